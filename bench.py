@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention forward (HipGPT's hot path) on one GPU.
+
+Headline (BASELINE.json metric): causal attention forward TFLOP/s and the
+fraction of the fp32 MFMA roofline at B32 H8 S256 D32 (config c1), inputs
+resident in HBM.  One step = one attention forward over the whole batch.
+The other BASELINE configs are timed the same way and reported under
+"configs"; the oracle's scalar restatement is timed on the host cores as
+"cpu_baseline".
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F32_MFMA = 157.3e12   # MI355X dense fp32 matrix, FLOP/s
+PEAK_BF16_MFMA = 2.5e15    # dense bf16 matrix
+PEAK_HBM = 8.0e12          # HBM3E bytes/s
+METRIC = "causal attention fwd TFLOP/s + % of MFMA roofline on 1 MI355X (B32 H8 S256 D32)"
+
+# name: (B, H, Sq, Sk, D, causal, dtype, probs, kind)
+CONFIGS = {
+    "c1": (32, 8, 256, 256, 32, True, "f32", False, "fwd"),
+    "c1_probs": (32, 8, 256, 256, 32, True, "f32", True, "fwd"),
+    "c1_legacy": (32, 8, 256, 256, 32, False, "f32", True, "fwd"),
+    "c2": (32, 8, 256, 256, 64, True, "f32", False, "fwd"),
+    "c2_probs": (32, 8, 256, 256, 64, True, "f32", True, "fwd"),
+    "c3": (8, 12, 1024, 1024, 64, True, "f32", False, "fwd"),
+    "c3_bf16": (8, 12, 1024, 1024, 64, True, "bf16", False, "fwd"),
+    "c4": (4, 16, 2048, 2048, 128, True, "f32", False, "fwd"),
+    "c5": (64, 12, 1, 2048, 64, False, "f32", False, "decode"),
+}
+
+
+def work(cfg):
+    """Algorithmic FLOPs (4*B*H*D*P, P visible pairs) and HBM bytes (Q, K, V
+    read once, O written once, plus probs when written)."""
+    B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+    if kind == "decode":
+        pairs = Sk
+    elif causal:
+        off = Sk - Sq
+        pairs = sum(min(Sk, i + 1 + off) for i in range(Sq))
+    else:
+        pairs = Sq * Sk
+    flops = 4.0 * B * H * D * pairs
+    el = 2 if dtype == "bf16" else 4
+    nbytes = el * B * H * D * (Sq + 2 * Sk) + 4 * B * H * Sq * D
+    if probs:
+        nbytes += 4 * B * H * Sq * Sk
+    return flops, nbytes
+
+
+def make_call(cfg, torch, A, dev):
+    B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x48495047)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    if kind == "decode":
+        q = torch.randn(B, 1, H, D, device=dev, generator=g)
+        k = torch.randn(B, Sk, H, D, device=dev, generator=g)
+        v = torch.randn(B, Sk, H, D, device=dev, generator=g)
+        out = torch.empty(B, 1, H, D, device=dev)
+        ns = A.decode_default_splits(B, H, Sk)
+        ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
+        return lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws), {"splits": ns}
+    E = H * D
+    if dtype == "f32" and Sq == Sk:
+        # the reference's planar [Q|K|V] buffer
+        qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)
+        out = torch.empty(B * Sq, E, device=dev)
+        p = torch.empty(B, H, Sq, Sk, device=dev) if probs else None
+        return lambda: A.qkv_planar(qkv, out, p, B, Sq, E, H, causal=causal), {"layout": "planar [3][B*S][E]"}
+    q = torch.randn(B, Sq, H, D, device=dev, generator=g).to(tdt)
+    k = torch.randn(B, Sk, H, D, device=dev, generator=g).to(tdt)
+    v = torch.randn(B, Sk, H, D, device=dev, generator=g).to(tdt)
+    out = torch.empty(B, Sq, H, D, device=dev)
+    p = torch.empty(B, H, Sq, Sk, device=dev) if probs else None
+    return lambda: A.attention(q, k, v, out=out, probs=p, causal=causal), {"layout": "[B,S,H,D]"}
+
+
+def time_call(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()  # the stream the library launches on
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per call
+
+
+def cpu_baseline(nthreads):
+    """The oracle's scalar restatement of the reference kernel HipGPT runs for
+    c1 (flash_attention_kernel<32>, causal-restricted) on the whole c1
+    problem, on the host cores."""
+    import numpy as np
+
+    import oracle as O
+
+    B, H, S, D = 32, 8, 256, 32
+    E = H * D
+    qkv = O.seeded_planar(0x48495047, B, S, E)
+    q, k, v = O.planar_qkv(qkv, B, S, E, H)
+    t0 = time.perf_counter()
+    O.attention(q, k, v, causal=True, variant=O.FLASH, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    flops, _ = work(CONFIGS["c1"])
+    return flops / dt, dt, np
+
+
+def read_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default="", help="comma-separated config names (default: all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one MI355X only; the attention forward shards "
+              "over (batch, head) with no exchange, so N GPUs run N independent copies.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from hipgpt_amd import attention as A
+
+    dev = torch.device("cuda:0")
+    names = [n for n in args.only.split(",") if n] or list(CONFIGS)
+    results = {}
+    for name in names:
+        cfg = CONFIGS[name]
+        try:
+            fn, extra = make_call(cfg, torch, A, dev)
+        except Exception as e:  # e.g. a dtype this build has no kernel for
+            results[name] = {"error": str(e)}
+            continue
+        try:
+            ms = time_call(fn, args.steps, args.warmup, torch)
+        except Exception as e:
+            results[name] = {"error": str(e)}
+            continue
+        flops, nbytes = work(cfg)
+        B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+        peak = PEAK_BF16_MFMA if dtype == "bf16" else PEAK_F32_MFMA
+        t_mfma = flops / peak
+        t_hbm = nbytes / PEAK_HBM
+        bound = "hbm" if t_hbm > t_mfma else "mfma"
+        tflops = flops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        frac = (t_hbm if bound == "hbm" else t_mfma) / (ms * 1e-3)
+        results[name] = {
+            "shape": {"B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D}, "causal": causal,
+            "dtype": dtype, "probs": probs, "us_per_call": round(ms * 1e3, 3),
+            "tflops": round(tflops, 3), "gbs": round(gbs, 1), "bound": bound,
+            "roofline_frac": round(frac, 4), **extra,
+        }
+        print(f"# {name}: {ms * 1e3:.2f} us  {tflops:.2f} TFLOP/s  {gbs:.0f} GB/s  "
+              f"{bound}-bound frac {frac:.3f}", file=sys.stderr, flush=True)
+
+    head = results.get("c1", {})
+    line = {
+        "metric": METRIC,
+        "value": head.get("tflops"),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 6) if "us_per_call" in head else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic N(0,1) Q/K/V resident in HBM (planar [3][B*S][E] buffer, seeded)",
+        "config": {"workload": "c1: causal self-attention forward, fp32, B=32 H=8 S=256 D=32 (E=256), "
+                               "no probs output", "B": 32, "H": 8, "S": 256, "D": 32,
+                   "parallelism": "single GPU"},
+    }
+    if "us_per_call" in head:
+        flops, _ = work(CONFIGS["c1"])
+        ach = flops / (head["us_per_call"] * 1e-6)
+        line["roofline"] = {
+            "bound": "mfma", "achieved": round(ach / 1e12, 3), "peak": PEAK_F32_MFMA / 1e12,
+            "unit": "TFLOP/s", "frac": round(ach / PEAK_F32_MFMA, 4), "traffic": read_traffic("c1"),
+        }
+    if not args.no_cpu:
+        cpu1, dt1, _ = cpu_baseline(1)
+        ncores = min(16, os.cpu_count() or 1)
+        cpun, dtn, _ = cpu_baseline(ncores)
+        line["cpu_baseline"] = {
+            "value": round(cpu1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"whole c1 problem (causal, 256 (b,h) pairs) through the scalar restatement of "
+                      f"flash_attention_kernel<32>: {dt1:.2f} s on 1 thread",
+            "all_cores": {"value": round(cpun / 1e12, 6), "cores": ncores, "seconds": round(dtn, 3)},
+        }
+    line["configs"] = results
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

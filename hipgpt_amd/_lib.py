@@ -1,0 +1,93 @@
+"""ctypes binding of libhipgpt_attn.so (include/hip_kernels.h, include/hipgpt_attn.h).
+
+The shared library is built in-tree (``make -C hipgpt_amd/csrc``) and loaded
+from this package directory.  There is no fallback: a missing or stale build
+raises, so no caller can silently run anything but the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libhipgpt_attn.so")
+
+# Status codes of include/hipgpt_attn.h.
+OK = 0
+ERR_INVALID = -1
+ERR_UNSUPPORTED = -2
+ERR_LAUNCH = -3
+ERR_WORKSPACE = -4
+
+F32 = 0
+BF16 = 1
+
+# Entry points declared in include/*.h, with their ctypes signatures.
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_f = ctypes.c_float
+
+SIGNATURES = {
+    "hipgpt_attn_strerror": (ctypes.c_char_p, [_int]),
+    "hipgpt_launch_multihead_attention": (None, [_vp, _vp, _vp, _int, _int, _int, _int]),
+    "hipgpt_attn_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
+    "hipgpt_attn_fwd": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int]
+        + [_i64] * 12
+        + [_f, _int, _int, _vp],
+    ),
+    "hipgpt_attn_decode_default_splits": (_int, [_int, _int, _int]),
+    "hipgpt_attn_decode_workspace_bytes": (ctypes.c_size_t, [_int, _int, _int, _int]),
+    "hipgpt_attn_decode": (
+        _int,
+        [_vp, _vp, _vp, _vp, _int, _int, _int, _int]
+        + [_i64] * 10
+        + [_f, _int, _vp, ctypes.c_size_t, _vp],
+    ),
+}
+# The drop-in C++ symbol (HipGPT include/hip_kernels.h:39-43).
+CXX_LAUNCH_SYMBOL = "_Z26launch_multihead_attentionPKfPfS1_iiii"
+
+_lib = None
+_lock = threading.Lock()
+
+
+class HipgptError(RuntimeError):
+    """A non-OK status from the library."""
+
+    def __init__(self, status: int, what: str = ""):
+        self.status = status
+        msg = lib().hipgpt_attn_strerror(status).decode()
+        super().__init__(f"{what}: {msg} (status {status})" if what else msg)
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library with typed entry points."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `make -C hipgpt_amd/csrc` "
+                    "(or __graft_entry__.build())"
+                )
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            cxx = getattr(handle, CXX_LAUNCH_SYMBOL)
+            cxx.restype = None
+            cxx.argtypes = SIGNATURES["hipgpt_launch_multihead_attention"][1]
+            _lib = handle
+    return _lib
+
+
+def check(status: int, what: str = "") -> None:
+    if status != OK:
+        raise HipgptError(status, what)

@@ -1,0 +1,170 @@
+"""Host-side mirror of HipGPT's attention forward interface over libhipgpt_attn.so.
+
+Tensors are torch device tensors (torch is only the allocator and stream
+provider here); every call goes through the C ABI to the HIP kernels.
+
+* :func:`launch_multihead_attention` -- HipGPT's launcher
+  (``include/hip_kernels.h:39-43``, ``src/hip_kernels.cpp:404-451``): planar
+  ``d_qkv = [Q|K|V]`` each ``[B*S, E]``, non-causal, probs written when given.
+* :func:`qkv_planar` -- same layout, plus causal masking and a stream.
+* :func:`attention` -- strided ``[B, S, H, D]`` views, fp32 or bf16 inputs.
+* :func:`decode` -- one query row per sequence against ``kv_len`` keys,
+  split-KV.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+
+def _ptr(t):
+    return 0 if t is None else t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _need_cuda(name, t, dtype=None):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a CUDA (HIP) tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def launch_multihead_attention(d_qkv, d_output, d_attn_probs, B, S, E, H):
+    """HipGPT ``launch_multihead_attention`` (drop-in semantics).
+
+    The C++ symbol aborts the process on ``H <= 0 or E % H != 0``
+    (``src/hip_kernels.cpp:410-413``); this Python mirror raises the same
+    message as ``ValueError`` before reaching it.  Launches on the null
+    stream, like the reference.
+    """
+    if H <= 0 or E % H != 0:
+        raise ValueError(f"Bad MHA config: E={E} H={H}")
+    _need_cuda("d_qkv", d_qkv, torch.float32)
+    _need_cuda("d_output", d_output, torch.float32)
+    n = B * S * E
+    if d_qkv.numel() < 3 * n or d_output.numel() < n:
+        raise ValueError("d_qkv / d_output too small for B*S*E")
+    if d_attn_probs is not None:
+        _need_cuda("d_attn_probs", d_attn_probs, torch.float32)
+        if d_attn_probs.numel() < B * H * S * S:
+            raise ValueError("d_attn_probs too small for B*H*S*S")
+    for t in (d_qkv, d_output, d_attn_probs):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("launch_multihead_attention needs contiguous buffers")
+    _lib.lib().hipgpt_launch_multihead_attention(
+        _ptr(d_qkv), _ptr(d_output), _ptr(d_attn_probs), B, S, E, H
+    )
+
+
+def qkv_planar(d_qkv, d_output, d_attn_probs, B, S, E, H, causal=False, stream=None):
+    """Planar-layout forward with causal masking and an explicit stream."""
+    _need_cuda("d_qkv", d_qkv, torch.float32)
+    _need_cuda("d_output", d_output, torch.float32)
+    if d_qkv.numel() < 3 * B * S * E or d_output.numel() < B * S * E:
+        raise ValueError("d_qkv / d_output too small for B*S*E")
+    if d_attn_probs is not None:
+        _need_cuda("d_attn_probs", d_attn_probs, torch.float32)
+        if d_attn_probs.numel() < B * H * S * S:
+            raise ValueError("d_attn_probs too small for B*H*S*S")
+    rc = _lib.lib().hipgpt_attn_qkv_planar(
+        _ptr(d_qkv), _ptr(d_output), _ptr(d_attn_probs), B, S, E, H, int(bool(causal)),
+        _stream(stream),
+    )
+    _lib.check(rc, "hipgpt_attn_qkv_planar")
+
+
+def _bshd_strides(t, name):
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B, S, H, D]")
+    if t.stride(3) != 1:
+        raise ValueError(f"{name} must be contiguous in D")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def attention(q, k, v, out=None, probs=None, causal=False, scale=None, stream=None):
+    """softmax(q k^T * scale) v over ``[B, S, H, D]`` views; returns fp32 ``out``.
+
+    q: [B, Sq, H, D], k/v: [B, Sk, H, D], all float32 or all bfloat16 (bf16
+    runs bf16 MFMA with fp32 accumulation).  ``probs`` (optional) is fp32
+    ``[B, H, Sq, Sk]``.  ``causal`` masks keys j > i + (Sk - Sq).
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need_cuda(name, t)
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("q, k, v must all be float32 or all bfloat16")
+    B, Sq, H, D = q.shape
+    if k.shape[0] != B or k.shape[2] != H or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError("k, v must be [B, Sk, H, D] matching q")
+    Sk = k.shape[1]
+    if out is None:
+        out = torch.empty((B, Sq, H, D), device=q.device, dtype=torch.float32)
+    _need_cuda("out", out, torch.float32)
+    if tuple(out.shape) != (B, Sq, H, D):
+        raise ValueError("out must be [B, Sq, H, D]")
+    if probs is not None:
+        _need_cuda("probs", probs, torch.float32)
+        if tuple(probs.shape) != (B, H, Sq, Sk) or not probs.is_contiguous():
+            raise ValueError("probs must be contiguous [B, H, Sq, Sk]")
+    qs, ks, vs, os_ = (_bshd_strides(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out")))
+    dtype = _lib.F32 if q.dtype == torch.float32 else _lib.BF16
+    sc = -1.0 if scale is None else float(scale)
+    rc = _lib.lib().hipgpt_attn_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(probs), B, H, Sq, Sk, D,
+        *qs, *ks, *vs, *os_, sc, int(bool(causal)), dtype, _stream(stream),
+    )
+    _lib.check(rc, "hipgpt_attn_fwd")
+    return out
+
+
+def decode_workspace_bytes(B, H, D, num_splits):
+    return int(_lib.lib().hipgpt_attn_decode_workspace_bytes(B, H, D, num_splits))
+
+
+def decode_default_splits(B, H, kv_len):
+    return int(_lib.lib().hipgpt_attn_decode_default_splits(B, H, kv_len))
+
+
+def decode(q, k, v, out=None, num_splits=None, workspace=None, scale=None, stream=None):
+    """One decode step: q [B, 1, H, D] against k/v [B, kv_len, H, D] (fp32).
+
+    Split-KV with ``num_splits`` partitions (default: the library's choice);
+    ``workspace`` is a caller-owned device buffer (allocated here if None).
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need_cuda(name, t, torch.float32)
+    B, one, H, D = q.shape
+    if one != 1:
+        raise ValueError("q must be [B, 1, H, D]")
+    kv = k.shape[1]
+    if tuple(k.shape) != (B, kv, H, D) or v.shape != k.shape:
+        raise ValueError("k, v must be [B, kv_len, H, D]")
+    if out is None:
+        out = torch.empty((B, 1, H, D), device=q.device, dtype=torch.float32)
+    _need_cuda("out", out, torch.float32)
+    ns = decode_default_splits(B, H, kv) if num_splits is None else int(num_splits)
+    ns = max(1, min(ns, kv))
+    need = decode_workspace_bytes(B, H, D, ns)
+    if workspace is None and need > 0:
+        workspace = torch.empty(need // 4, device=q.device, dtype=torch.float32)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    qs, ks, vs, os_ = (_bshd_strides(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out")))
+    sc = -1.0 if scale is None else float(scale)
+    rc = _lib.lib().hipgpt_attn_decode(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, H, kv, D,
+        qs[0], qs[2], *ks, *vs, os_[0], os_[2],
+        sc, ns, _ptr(workspace), ws_bytes, _stream(stream),
+    )
+    _lib.check(rc, "hipgpt_attn_decode")
+    return out
+
+
+def default_scale(D):
+    return 1.0 / math.sqrt(D)

@@ -1,0 +1,197 @@
+// api.cpp -- host side of libhipgpt_attn.so: validation, kernel selection,
+// the drop-in launch_multihead_attention and the C ABI of hipgpt_attn.h.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+
+#include "../../include/hip_kernels.h"
+#include "../../include/hipgpt_attn.h"
+#include "kernels.h"
+
+using hipgpt::AttnArgs;
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+float default_scale(int D, float scale) { return scale > 0.f ? scale : 1.0f / std::sqrt((float)D); }
+
+int from_hip(hipError_t e) { return e == hipSuccess ? HIPGPT_OK : HIPGPT_ERR_LAUNCH; }
+
+// Shared validation and dispatch for every forward entry point.
+int attn_dispatch(const AttnArgs& in, int causal, int dtype, hipStream_t stream) {
+    if (!in.q || !in.k || !in.v || !in.o) return HIPGPT_ERR_INVALID;
+    if (in.B <= 0 || in.H <= 0 || in.Sq <= 0 || in.Sk <= 0 || in.D <= 0) return HIPGPT_ERR_INVALID;
+    if (causal && in.Sk < in.Sq) return HIPGPT_ERR_INVALID;
+    if (dtype != HIPGPT_F32 && dtype != HIPGPT_BF16) return HIPGPT_ERR_INVALID;
+    if ((int64_t)in.B * in.H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    AttnArgs a = in;
+    a.causal_off = causal ? in.Sk - in.Sq : 0;
+
+    if (dtype == HIPGPT_BF16) {
+        if (!hipgpt::fa_bf16_supported(a.D)) return HIPGPT_ERR_UNSUPPORTED;
+        const bool ok = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+                        a.q_bs % 8 == 0 && a.q_ts % 8 == 0 && a.q_hs % 8 == 0 && a.k_bs % 8 == 0 &&
+                        a.k_ts % 8 == 0 && a.k_hs % 8 == 0 && a.v_bs % 8 == 0 && a.v_ts % 8 == 0 &&
+                        a.v_hs % 8 == 0 && a.o_bs % 4 == 0 && a.o_ts % 4 == 0 && a.o_hs % 4 == 0;
+        if (!ok) return HIPGPT_ERR_UNSUPPORTED;
+        return from_hip(hipgpt::launch_fa_bf16(a, causal != 0, stream));
+    }
+
+    const int dp = hipgpt::fa_f32_padded_dim(a.D);
+    if (dp == 0) return from_hip(hipgpt::launch_attn_generic_f32(a, causal != 0, stream));
+    const bool vec = a.D == dp && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+                     (!a.probs || aligned16(a.probs)) && a.q_bs % 4 == 0 && a.q_ts % 4 == 0 &&
+                     a.q_hs % 4 == 0 && a.k_bs % 4 == 0 && a.k_ts % 4 == 0 && a.k_hs % 4 == 0 &&
+                     a.v_bs % 4 == 0 && a.v_ts % 4 == 0 && a.v_hs % 4 == 0 && a.o_bs % 4 == 0 &&
+                     a.o_ts % 4 == 0 && a.o_hs % 4 == 0;
+    return from_hip(hipgpt::launch_fa_f32(a, causal != 0, vec, stream));
+}
+
+// The planar [3][B*S][E] buffer of src/hip_kernels.cpp:415-417 as strides.
+AttnArgs planar_args(const float* qkv, float* out, float* probs, int B, int S, int E, int H) {
+    const int64_t plane = (int64_t)B * S * E;
+    AttnArgs a{};
+    a.q = qkv;
+    a.k = qkv + plane;
+    a.v = qkv + 2 * plane;
+    a.o = out;
+    a.probs = probs;
+    a.q_bs = a.k_bs = a.v_bs = a.o_bs = (int64_t)S * E;
+    a.q_ts = a.k_ts = a.v_ts = a.o_ts = E;
+    a.q_hs = a.k_hs = a.v_hs = a.o_hs = E / H;
+    a.B = B;
+    a.H = H;
+    a.Sq = S;
+    a.Sk = S;
+    a.D = E / H;
+    a.qscale = default_scale(a.D, 0.f) * hipgpt::kLog2e;
+    return a;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ drop-in symbol
+
+void launch_multihead_attention(const float* d_qkv, float* d_output, float* d_attn_probs, int B, int S,
+                                int E, int H) {
+    if (H <= 0 || (E % H) != 0) {  // src/hip_kernels.cpp:410-413
+        fprintf(stderr, "Bad MHA config: E=%d H=%d\n", E, H);
+        abort();
+    }
+    if (B <= 0 || S <= 0 || E <= 0) return;  // nothing to launch (the reference's grid would be empty)
+    const int rc = attn_dispatch(planar_args(d_qkv, d_output, d_attn_probs, B, S, E, H), 0, HIPGPT_F32, 0);
+    if (rc != HIPGPT_OK)
+        fprintf(stderr, "launch_multihead_attention: %s (B=%d S=%d E=%d H=%d)\n", hipgpt_attn_strerror(rc), B,
+                S, E, H);
+}
+
+// ------------------------------------------------------------------- C ABI
+
+extern "C" {
+
+const char* hipgpt_attn_strerror(int status) {
+    switch (status) {
+        case HIPGPT_OK: return "ok";
+        case HIPGPT_ERR_INVALID: return "invalid argument";
+        case HIPGPT_ERR_UNSUPPORTED: return "unsupported problem (head dim, dtype or alignment)";
+        case HIPGPT_ERR_LAUNCH: return "kernel launch failed";
+        case HIPGPT_ERR_WORKSPACE: return "workspace missing or too small";
+        default: return "unknown status";
+    }
+}
+
+void hipgpt_launch_multihead_attention(const float* d_qkv, float* d_output, float* d_attn_probs, int B,
+                                       int S, int E, int H) {
+    launch_multihead_attention(d_qkv, d_output, d_attn_probs, B, S, E, H);
+}
+
+int hipgpt_attn_qkv_planar(const float* d_qkv, float* d_output, float* d_attn_probs, int B, int S, int E,
+                           int H, int causal, hipStream_t stream) {
+    if (!d_qkv || !d_output || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0) return HIPGPT_ERR_INVALID;
+    return attn_dispatch(planar_args(d_qkv, d_output, d_attn_probs, B, S, E, H), causal, HIPGPT_F32, stream);
+}
+
+int hipgpt_attn_fwd(const void* q, const void* k, const void* v, float* o, float* probs, int B, int H, int Sq,
+                    int Sk, int D, int64_t q_bs, int64_t q_ts, int64_t q_hs, int64_t k_bs, int64_t k_ts,
+                    int64_t k_hs, int64_t v_bs, int64_t v_ts, int64_t v_hs, int64_t o_bs, int64_t o_ts,
+                    int64_t o_hs, float scale, int causal, int dtype, hipStream_t stream) {
+    if (D <= 0 || !std::isfinite(scale)) return HIPGPT_ERR_INVALID;
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.probs = probs;
+    a.q_bs = q_bs;
+    a.q_ts = q_ts;
+    a.q_hs = q_hs;
+    a.k_bs = k_bs;
+    a.k_ts = k_ts;
+    a.k_hs = k_hs;
+    a.v_bs = v_bs;
+    a.v_ts = v_ts;
+    a.v_hs = v_hs;
+    a.o_bs = o_bs;
+    a.o_ts = o_ts;
+    a.o_hs = o_hs;
+    a.B = B;
+    a.H = H;
+    a.Sq = Sq;
+    a.Sk = Sk;
+    a.D = D;
+    a.qscale = default_scale(D, scale) * hipgpt::kLog2e;
+    return attn_dispatch(a, causal, dtype, stream);
+}
+
+int hipgpt_attn_decode_default_splits(int B, int H, int kv_len) {
+    if (B <= 0 || H <= 0 || kv_len <= 0) return 1;
+    return hipgpt::decode_default_splits(B, H, kv_len);
+}
+
+size_t hipgpt_attn_decode_workspace_bytes(int B, int H, int D, int num_splits) {
+    if (B <= 0 || H <= 0 || D <= 0 || num_splits <= 1) return 0;
+    return (size_t)B * H * num_splits * (size_t)(D + 2) * sizeof(float);
+}
+
+int hipgpt_attn_decode(const float* q, const float* k, const float* v, float* o, int B, int H, int kv_len, int D,
+                       int64_t q_bs, int64_t q_hs, int64_t k_bs, int64_t k_ts, int64_t k_hs, int64_t v_bs,
+                       int64_t v_ts, int64_t v_hs, int64_t o_bs, int64_t o_hs, float scale, int num_splits,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!q || !k || !v || !o || B <= 0 || H <= 0 || kv_len <= 0 || D <= 0 || !std::isfinite(scale))
+        return HIPGPT_ERR_INVALID;
+    if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if (!hipgpt::decode_supported(D, hipgpt::kF32)) return HIPGPT_ERR_UNSUPPORTED;
+    const bool ok = aligned16(q) && aligned16(k) && aligned16(v) && q_bs % 4 == 0 && q_hs % 4 == 0 &&
+                    k_bs % 4 == 0 && k_ts % 4 == 0 && k_hs % 4 == 0 && v_bs % 4 == 0 && v_ts % 4 == 0 &&
+                    v_hs % 4 == 0;
+    if (!ok) return HIPGPT_ERR_UNSUPPORTED;
+    int ns = num_splits > 0 ? num_splits : hipgpt::decode_default_splits(B, H, kv_len);
+    if (ns > kv_len) ns = kv_len;
+    const size_t need = hipgpt_attn_decode_workspace_bytes(B, H, D, ns);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return HIPGPT_ERR_WORKSPACE;
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.q_bs = q_bs;
+    a.q_hs = q_hs;
+    a.k_bs = k_bs;
+    a.k_ts = k_ts;
+    a.k_hs = k_hs;
+    a.v_bs = v_bs;
+    a.v_ts = v_ts;
+    a.v_hs = v_hs;
+    a.o_bs = o_bs;
+    a.o_hs = o_hs;
+    a.B = B;
+    a.H = H;
+    a.Sq = 1;
+    a.Sk = kv_len;
+    a.D = D;
+    a.qscale = default_scale(D, scale) * hipgpt::kLog2e;
+    return from_hip(hipgpt::launch_decode(a, hipgpt::kF32, ns, static_cast<float*>(workspace), stream));
+}
+
+}  // extern "C"

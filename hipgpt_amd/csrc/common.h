@@ -1,0 +1,60 @@
+// common.h -- shared device types and helpers for the gfx950 attention path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hipgpt {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+// Running-max start value.  Finite (unlike -inf) so that the first rescale
+// exp2(m_old - m_new) is exp2(-huge) = 0 rather than exp2(-inf + inf) = NaN;
+// the same value the reference starts from (src/hip_kernels.cpp:279, :350).
+constexpr float kMaxInit = -1e30f;
+
+enum Dtype : int { kF32 = 0, kBF16 = 1 };
+
+// Strided attention problem as the kernels see it.  Element (b, s, h, d) of
+// a tensor X lives at X[b*x_bs + s*x_ts + h*x_hs + d] (elements of the input
+// dtype).  probs, when not null, is dense fp32 [B][H][Sq][Sk].
+struct AttnArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    float* o;
+    float* probs;
+    int64_t q_bs, q_ts, q_hs;
+    int64_t k_bs, k_ts, k_hs;
+    int64_t v_bs, v_ts, v_hs;
+    int64_t o_bs, o_ts, o_hs;
+    int B, H, Sq, Sk, D;
+    int causal_off;  // causal: query i sees keys j <= i + causal_off (Sk - Sq)
+    float qscale;    // softmax scale * log2(e), folded into Q
+    int n_qblk;      // query blocks per (b,h)
+};
+
+// exp2 on the transcendental unit (v_exp_f32): exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Exchange with the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+    return x;
+}
+
+}  // namespace hipgpt

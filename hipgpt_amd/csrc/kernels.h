@@ -1,0 +1,30 @@
+// kernels.h -- internal launch functions shared by the C ABI (api.cpp) and the
+// kernel translation units.  Not installed; the public surface is
+// include/hip_kernels.h and include/hipgpt_attn.h.
+#pragma once
+
+#include "common.h"
+
+namespace hipgpt {
+
+// Padded head dim served by the fp32 MFMA kernel (32, 64, 128), 0 if none.
+int fa_f32_padded_dim(int D);
+// fp32 MFMA flash attention.  vec: D equals the padded dim and every stride
+// and base pointer allows 16-byte accesses.
+hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t stream);
+
+// bf16-input / fp32-accumulate MFMA flash attention (D in {32, 64, 128},
+// 16-byte aligned rows).  Writes fp32 O (and fp32 probs when requested).
+bool fa_bf16_supported(int D);
+hipError_t launch_fa_bf16(const AttnArgs& a, bool causal, hipStream_t stream);
+
+// Any head dim, fp32: one wave per query row (the path for D > 128).
+hipError_t launch_attn_generic_f32(const AttnArgs& a, bool causal, hipStream_t stream);
+
+// Split-KV single-query decode.  q: [B][1][H*D]-style strides in a; partial
+// results go to ws (nsplit * B * H * (D + 2) floats) when nsplit > 1.
+bool decode_supported(int D, int dtype);
+int decode_default_splits(int B, int H, int kv_len);
+hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream);
+
+}  // namespace hipgpt

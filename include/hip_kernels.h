@@ -1,0 +1,27 @@
+#pragma once
+// hip_kernels.h -- drop-in declaration of HipGPT's attention forward launcher.
+//
+// The signature is the one HipGPT declares in include/hip_kernels.h:39-43
+// (C++ linkage; exported as _Z26launch_multihead_attentionPKfPfS1_iiii), so
+// TransformerLayer::self_attention_forward (src/transformer_layer.cpp:218-219)
+// links against libhipgpt_attn.so unchanged.  HipGPT's other declarations in
+// that header (GEMM, layer norm, loss, optimisers, the attention backward and
+// the unused unfused helpers) are not provided by this library.
+
+#include <hip/hip_runtime.h>
+
+// Multi-head self-attention forward over HipGPT's planar packed buffer.
+//   d_qkv        [3][B*S][E] fp32: Q, K, V planes at offsets 0, B*S*E, 2*B*S*E;
+//                head h occupies columns [h*D, (h+1)*D), D = E / H.
+//   d_output     [B*S][E] fp32, fully written.
+//   d_attn_probs [B][H][S][S] fp32 normalised probabilities, written when
+//                non-null (HipGPT always passes one; its backward reads it).
+// Non-causal softmax(Q K^T / sqrt(D)) V per (batch, head).  Asynchronous on
+// the null stream; allocates nothing.  Prints "Bad MHA config" and aborts
+// when H <= 0 or E % H != 0, as the reference launcher does
+// (src/hip_kernels.cpp:410-413).  Replaces src/hip_kernels.cpp:404-451.
+void launch_multihead_attention(
+    const float* d_qkv,
+    float* d_output,
+    float* d_attn_probs,
+    int B, int S, int E, int H);

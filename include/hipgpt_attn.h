@@ -1,0 +1,82 @@
+#pragma once
+// hipgpt_attn.h -- C ABI of the MI355X attention forward library
+// (libhipgpt_attn.so).  Plain pointers and sizes; no C++ or torch types.
+//
+// Every entry point is asynchronous on the given stream (0 = null stream),
+// allocates nothing unless stated, and returns HIPGPT_OK or a negative
+// status (see hipgpt_attn_strerror).  Pointers are device pointers.
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    HIPGPT_OK = 0,
+    HIPGPT_ERR_INVALID = -1,      /* bad size, stride, pointer or flag        */
+    HIPGPT_ERR_UNSUPPORTED = -2,  /* valid problem this build has no kernel for */
+    HIPGPT_ERR_LAUNCH = -3,       /* the HIP launch itself failed             */
+    HIPGPT_ERR_WORKSPACE = -4     /* workspace missing or too small           */
+};
+
+enum { HIPGPT_F32 = 0, HIPGPT_BF16 = 1 };
+
+/* Text for a status code. */
+const char* hipgpt_attn_strerror(int status);
+
+/* C-linkage twin of launch_multihead_attention (include/hip_kernels.h), for
+ * FFI callers that cannot bind a C++ symbol.  Same contract, including the
+ * abort on H <= 0 or E % H != 0.  Replaces src/hip_kernels.cpp:404-451. */
+void hipgpt_launch_multihead_attention(const float* d_qkv, float* d_output,
+                                       float* d_attn_probs, int B, int S,
+                                       int E, int H);
+
+/* HipGPT's planar [3][B*S][E] layout with the options the legacy symbol
+ * lacks: causal masking (keys j <= i; probs written 0 above the diagonal so
+ * HipGPT's backward, src/hip_kernels.cpp:1162-1243, stays exact) and a
+ * stream.  Returns a status instead of aborting. */
+int hipgpt_attn_qkv_planar(const float* d_qkv, float* d_output,
+                           float* d_attn_probs, int B, int S, int E, int H,
+                           int causal, hipStream_t stream);
+
+/* General strided attention forward.
+ *   q, k, v: element (b, s, h, d) at X[b*x_bs + s*x_ts + h*x_hs + d], in
+ *            `dtype` (HIPGPT_F32 or HIPGPT_BF16); d is contiguous.
+ *   o:       fp32, same indexing with o_* strides.
+ *   probs:   optional dense fp32 [B][H][Sq][Sk] normalised probabilities.
+ *   scale:   softmax scale; <= 0 selects 1/sqrt(D).
+ *   causal:  query i sees keys j <= i + (Sk - Sq); requires Sk >= Sq.
+ * bf16 inputs are computed with bf16 MFMA and fp32 accumulation, D in
+ * {32, 64, 128}, 16-byte aligned rows (strides multiple of 8). */
+int hipgpt_attn_fwd(const void* q, const void* k, const void* v, float* o,
+                    float* probs, int B, int H, int Sq, int Sk, int D,
+                    int64_t q_bs, int64_t q_ts, int64_t q_hs,
+                    int64_t k_bs, int64_t k_ts, int64_t k_hs,
+                    int64_t v_bs, int64_t v_ts, int64_t v_hs,
+                    int64_t o_bs, int64_t o_ts, int64_t o_hs,
+                    float scale, int causal, int dtype, hipStream_t stream);
+
+/* Single-query decode step: q [B][1][..] attends to kv_len keys (all
+ * visible).  Split-KV: num_splits partial workgroups per (b, h) write
+ * (max, sum, O) to `workspace`, a reduce kernel merges them.
+ * num_splits <= 0 picks hipgpt_attn_decode_default_splits().  fp32, D in
+ * {32, 64, 128, 256}, 16-byte aligned rows.  The workspace is caller-owned
+ * device memory of hipgpt_attn_decode_workspace_bytes() bytes (may be NULL
+ * when the split count is 1). */
+int hipgpt_attn_decode_default_splits(int B, int H, int kv_len);
+size_t hipgpt_attn_decode_workspace_bytes(int B, int H, int D, int num_splits);
+int hipgpt_attn_decode(const float* q, const float* k, const float* v,
+                       float* o, int B, int H, int kv_len, int D,
+                       int64_t q_bs, int64_t q_hs,
+                       int64_t k_bs, int64_t k_ts, int64_t k_hs,
+                       int64_t v_bs, int64_t v_ts, int64_t v_hs,
+                       int64_t o_bs, int64_t o_hs,
+                       float scale, int num_splits, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif

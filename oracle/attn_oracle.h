@@ -1,0 +1,95 @@
+/*
+ * attn_oracle.h -- CPU restatement of HipGPT's multi-head self-attention
+ * forward (TEST INFRASTRUCTURE ONLY).
+ *
+ * This library is the checker for the HIP path and the scalar CPU baseline
+ * timed beside it.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product (hipgpt_amd/) never links it.
+ *
+ * Reference (aarnetalman/HipGPT, paths relative to the repository root):
+ *   src/hip_kernels.cpp:263-325  flash_attention_kernel<HEAD_DIM>  -> ORACLE_FLASH
+ *   src/hip_kernels.cpp:329-402  multihead_attention_kernel_fallback -> ORACLE_FALLBACK
+ *   src/hip_kernels.cpp:404-451  launch_multihead_attention dispatch
+ *                                -> oracle_launch_multihead_attention
+ *
+ * Pinning (what fixes each function independently of its own formula):
+ *   oracle_attention_f64 ........ textbook softmax(QK^T/sqrt(D))V in double;
+ *                                 pinned by invariants with closed-form answers
+ *                                 (constant V, zero K -> prefix mean, S=1,
+ *                                 causal row 0, last row causal==non-causal,
+ *                                 huge scale -> argmax row) and by brute force
+ *                                 on tiny inputs computed with numpy.
+ *   ORACLE_FLASH / ORACLE_FALLBACK pinned against oracle_attention_f64 (<=1e-6
+ *                                 on unit-variance inputs), against the same
+ *                                 invariants, and against golden vectors
+ *                                 produced by the reference's own HIP kernels
+ *                                 (oracle/_ref build run on an MI355X).
+ *   oracle_fill_normal .......... SplitMix64 + Box-Muller; pinned by the
+ *                                 published SplitMix64 test vector and by
+ *                                 moment checks.
+ *   Causal mode has no reference counterpart (the reference is non-causal,
+ *   src/hip_kernels.cpp:287,:353): it is the reference arithmetic restricted to
+ *   keys j <= i + (Sk - Sq), probs written as 0 above the diagonal.  Its last
+ *   query row is pinned by the non-causal reference (they coincide there).
+ *   The device-math rounding of the reference (ocml expf, __expf on v_exp_f32,
+ *   rsqrtf on v_rsq_f32) is not reproduced bit for bit; it differs from libm
+ *   by a few ulp, far below the 1e-4 gate: parity of those ulps is unpinned.
+ */
+#ifndef HIPGPT_ATTN_ORACLE_H
+#define HIPGPT_ATTN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORACLE_FLASH = 0, ORACLE_FALLBACK = 1 };
+
+/* Strided attention problem.  Element (b, s, h, d) of Q lives at
+ * q[b*q_bs + s*q_ts + h*q_hs + d]; likewise for K, V, O.  probs, when not
+ * NULL, is dense [B][H][Sq][Sk].  Causal masks keys j > i + (Sk - Sq). */
+typedef struct {
+    const float *q, *k, *v;
+    float *o, *probs;
+    int B, H, Sq, Sk, D;
+    int64_t q_bs, q_ts, q_hs;
+    int64_t k_bs, k_ts, k_hs;
+    int64_t v_bs, v_ts, v_hs;
+    int64_t o_bs, o_ts, o_hs;
+    int causal;
+    int variant;  /* ORACLE_FLASH or ORACLE_FALLBACK */
+} oracle_attn_problem;
+
+/* SplitMix64 step (Steele, Lea, Flood 2014). */
+uint64_t oracle_splitmix64(uint64_t *state);
+/* n i.i.d. N(0,1) values: SplitMix64 -> Box-Muller in double -> fp32. */
+void oracle_fill_normal(uint64_t seed, float *out, size_t n);
+/* fp32 -> bf16 -> fp32 with round-to-nearest-even (NaN kept quiet). */
+void oracle_round_bf16(const float *in, float *out, size_t n);
+
+/* Scalar fp32 restatement of one of the two reference kernels over every
+ * (b,h) pair, split across nthreads host threads (nthreads <= 0: 1).
+ * Returns 0, or -1 on an invalid problem. */
+int oracle_attention(const oracle_attn_problem *p, int nthreads);
+/* Same, restricted to the listed (b,h) pairs (pairs[2*i], pairs[2*i+1]);
+ * used to time a bounded sample. */
+int oracle_attention_pairs(const oracle_attn_problem *p, const int *pairs,
+                           int npairs, int nthreads);
+
+/* Textbook attention in double precision (no clamps, exact softmax). */
+int oracle_attention_f64(const oracle_attn_problem *p, int nthreads);
+
+/* Mirror of launch_multihead_attention (src/hip_kernels.cpp:404-451) on the
+ * planar d_qkv = [Q|K|V], each [B*S][E]: same validation, same dispatch
+ * (flash restatement when D in {32,64} and S <= 512, fallback otherwise).
+ * Returns -1 where the reference aborts (H <= 0 or E % H != 0). */
+int oracle_launch_multihead_attention(const float *qkv, float *out,
+                                      float *probs, int B, int S, int E, int H,
+                                      int causal, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

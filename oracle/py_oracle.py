@@ -1,0 +1,195 @@
+"""ctypes binding of oracle/liboracle_attn.so (attn_oracle.h) and of the
+reference build oracle/_ref/libref_hip_kernels.so.
+
+TEST INFRASTRUCTURE ONLY (the checker / CPU baseline; never the product).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle_attn.so")
+REF_SO = os.path.join(HERE, "_ref", "libref_hip_kernels.so")
+
+FLASH = 0
+FALLBACK = 1
+
+__all__ = [
+    "ORACLE_SO", "REF_SO", "FLASH", "FALLBACK", "splitmix64", "fill_normal",
+    "round_bf16", "attention", "launch_multihead_attention", "ref_available",
+    "ref_lib", "planar_qkv", "seeded_planar", "seeded_bshd",
+]
+
+
+class _Problem(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p), ("probs", ctypes.c_void_p),
+        ("B", ctypes.c_int), ("H", ctypes.c_int), ("Sq", ctypes.c_int),
+        ("Sk", ctypes.c_int), ("D", ctypes.c_int),
+        ("q_bs", ctypes.c_int64), ("q_ts", ctypes.c_int64), ("q_hs", ctypes.c_int64),
+        ("k_bs", ctypes.c_int64), ("k_ts", ctypes.c_int64), ("k_hs", ctypes.c_int64),
+        ("v_bs", ctypes.c_int64), ("v_ts", ctypes.c_int64), ("v_hs", ctypes.c_int64),
+        ("o_bs", ctypes.c_int64), ("o_ts", ctypes.c_int64), ("o_hs", ctypes.c_int64),
+        ("causal", ctypes.c_int), ("variant", ctypes.c_int),
+    ]
+
+
+_lib = None
+
+
+def _oracle():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"{ORACLE_SO} missing: run `make -C oracle`")
+        L = ctypes.CDLL(ORACLE_SO)
+        L.oracle_splitmix64.restype = ctypes.c_uint64
+        L.oracle_splitmix64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.oracle_fill_normal.restype = None
+        L.oracle_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t]
+        L.oracle_round_bf16.restype = None
+        L.oracle_round_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        for fn in ("oracle_attention", "oracle_attention_f64"):
+            getattr(L, fn).restype = ctypes.c_int
+            getattr(L, fn).argtypes = [ctypes.POINTER(_Problem), ctypes.c_int]
+        L.oracle_attention_pairs.restype = ctypes.c_int
+        L.oracle_attention_pairs.argtypes = [ctypes.POINTER(_Problem), ctypes.c_void_p,
+                                             ctypes.c_int, ctypes.c_int]
+        L.oracle_launch_multihead_attention.restype = ctypes.c_int
+        L.oracle_launch_multihead_attention.argtypes = [
+            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ]
+        _lib = L
+    return _lib
+
+
+def splitmix64(seed: int, n: int):
+    st = ctypes.c_uint64(seed)
+    return [_oracle().oracle_splitmix64(ctypes.byref(st)) for _ in range(n)]
+
+
+def fill_normal(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _oracle().oracle_fill_normal(seed, out.ctypes.data, n)
+    return out
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    _oracle().oracle_round_bf16(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def _el_strides(a):
+    return tuple(s // a.itemsize for s in a.strides)
+
+
+def attention(q, k, v, causal=False, variant=FALLBACK, want_probs=False, f64=False,
+              nthreads=None, pairs=None):
+    """Oracle over [B, S, H, D] float32 numpy views (any strides, D contiguous).
+
+    variant FLASH / FALLBACK selects the restatement of
+    flash_attention_kernel (src/hip_kernels.cpp:263-325) or the fallback
+    (:329-402); f64 selects the textbook double-precision form.
+    Returns (out [B, Sq, H, D], probs [B, H, Sq, Sk] or None).
+    """
+    for a in (q, k, v):
+        if a.dtype != np.float32 or a.ndim != 4 or a.strides[3] != 4:
+            raise ValueError("oracle inputs must be float32 [B,S,H,D] with contiguous D")
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    out = np.zeros((B, Sq, H, D), dtype=np.float32)
+    probs = np.zeros((B, H, Sq, Sk), dtype=np.float32) if want_probs else None
+    p = _Problem()
+    p.q, p.k, p.v = q.ctypes.data, k.ctypes.data, v.ctypes.data
+    p.o = out.ctypes.data
+    p.probs = probs.ctypes.data if probs is not None else None
+    p.B, p.H, p.Sq, p.Sk, p.D = B, H, Sq, Sk, D
+    (p.q_bs, p.q_ts, p.q_hs, _) = _el_strides(q)
+    (p.k_bs, p.k_ts, p.k_hs, _) = _el_strides(k)
+    (p.v_bs, p.v_ts, p.v_hs, _) = _el_strides(v)
+    (p.o_bs, p.o_ts, p.o_hs, _) = _el_strides(out)
+    p.causal = int(bool(causal))
+    p.variant = variant
+    nt = nthreads if nthreads is not None else min(8, os.cpu_count() or 1)
+    L = _oracle()
+    if pairs is not None:
+        pr = np.ascontiguousarray(np.asarray(pairs, dtype=np.int32).reshape(-1, 2))
+        rc = L.oracle_attention_pairs(ctypes.byref(p), pr.ctypes.data, pr.shape[0], nt)
+    elif f64:
+        rc = L.oracle_attention_f64(ctypes.byref(p), nt)
+    else:
+        rc = L.oracle_attention(ctypes.byref(p), nt)
+    if rc != 0:
+        raise ValueError("oracle rejected the problem")
+    return out, probs
+
+
+def launch_multihead_attention(qkv, B, S, E, H, causal=False, want_probs=True, nthreads=None):
+    """Oracle mirror of the reference launcher on the planar buffer.
+    Returns (out [B*S, E], probs [B, H, S, S] or None); raises ValueError
+    where the reference aborts."""
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    if qkv.size < 3 * B * S * E:
+        raise ValueError("qkv too small")
+    out = np.zeros((B * S, E), dtype=np.float32)
+    probs = np.zeros((B, H, S, S), dtype=np.float32) if want_probs else None
+    nt = nthreads if nthreads is not None else min(8, os.cpu_count() or 1)
+    rc = _oracle().oracle_launch_multihead_attention(
+        qkv.ctypes.data, out.ctypes.data, probs.ctypes.data if probs is not None else None,
+        B, S, E, H, int(bool(causal)), nt)
+    if rc != 0:
+        raise ValueError(f"Bad MHA config: E={E} H={H}")
+    return out, probs
+
+
+def planar_qkv(qkv, B, S, E, H):
+    """[B, S, H, D] views of the Q, K, V planes of a planar buffer."""
+    D = E // H
+    planes = qkv.reshape(3, B, S, H, D)
+    return planes[0], planes[1], planes[2]
+
+
+def seeded_planar(seed, B, S, E):
+    """The planar d_qkv of one config: 3*B*S*E N(0,1) values, Q then K then V."""
+    return fill_normal(seed, 3 * B * S * E)
+
+
+def seeded_bshd(seed, B, Sq, Sk, H, D):
+    """q [B,Sq,H,D], k, v [B,Sk,H,D] from one seeded stream (q, then k, then v)."""
+    nq, nk = B * Sq * H * D, B * Sk * H * D
+    x = fill_normal(seed, nq + 2 * nk)
+    return (x[:nq].reshape(B, Sq, H, D), x[nq:nq + nk].reshape(B, Sk, H, D),
+            x[nq + nk:].reshape(B, Sk, H, D))
+
+
+# ---------------------------------------------------------------- reference
+_ref = None
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref_lib():
+    """The reference's own src/hip_kernels.cpp built for gfx950 (oracle/_ref).
+    Exposes `launch(qkv_ptr, out_ptr, probs_ptr, B, S, E, H)` (C++ symbol
+    _Z26launch_multihead_attentionPKfPfS1_iiii).  Import torch first so one
+    HIP runtime serves the process."""
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"{REF_SO} missing: run `make -C oracle ref` where /root/reference exists")
+        L = ctypes.CDLL(REF_SO)
+        fn = getattr(L, "_Z26launch_multihead_attentionPKfPfS1_iiii")
+        fn.restype = None
+        fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
+        L.launch = fn
+        _ref = L
+    return _ref

@@ -1,0 +1,73 @@
+"""CPU tests of the C-ABI library: it loads, exports every entry point the
+public headers declare (plus the drop-in C++ symbol), and rejects bad
+arguments before touching the GPU -- including the reference's abort on a
+bad head configuration (src/hip_kernels.cpp:410-413)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+from hipgpt_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("hip_kernels.h", "hipgpt_attn.h")]
+
+
+def declared_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return set(re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{]*\)\s*;", text))
+
+
+def test_headers_declare_expected_entry_points():
+    c_api = declared_functions(HEADERS[1])
+    assert set(_lib.SIGNATURES) == c_api
+    assert declared_functions(HEADERS[0]) == {"launch_multihead_attention"}
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions(HEADERS[1]):
+        assert hasattr(L, name), name
+    # HipGPT's C++ launcher, exact mangled name (include/hip_kernels.h:39-43)
+    assert hasattr(L, "_Z26launch_multihead_attentionPKfPfS1_iiii")
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True)
+    assert " T _Z26launch_multihead_attentionPKfPfS1_iiii" in out.stdout
+
+
+def test_strerror_and_host_validation():
+    L = _lib.lib()
+    assert L.hipgpt_attn_strerror(0) == b"ok"
+    assert b"invalid" in L.hipgpt_attn_strerror(_lib.ERR_INVALID)
+    z = [0] * 12
+    # null pointers, bad sizes, causal with Sk < Sq, bad dtype: all rejected host-side
+    assert L.hipgpt_attn_fwd(None, None, None, None, None, 1, 1, 1, 1, 32, *z, -1.0, 0, 0, None) == _lib.ERR_INVALID
+    p = 4096  # any non-null value: validation fails before any dereference
+    assert L.hipgpt_attn_fwd(p, p, p, p, None, 1, 1, 0, 1, 32, *z, -1.0, 0, 0, None) == _lib.ERR_INVALID
+    assert L.hipgpt_attn_fwd(p, p, p, p, None, 1, 1, 8, 4, 32, *z, -1.0, 1, 0, None) == _lib.ERR_INVALID
+    assert L.hipgpt_attn_fwd(p, p, p, p, None, 1, 1, 8, 8, 32, *z, -1.0, 0, 7, None) == _lib.ERR_INVALID
+    assert L.hipgpt_attn_qkv_planar(p, p, None, 1, 4, 63, 2, 0, None) == _lib.ERR_INVALID
+    assert L.hipgpt_attn_decode(None, None, None, None, 1, 1, 8, 64, *([0] * 10), -1.0, 1, None, 0, None) == _lib.ERR_INVALID
+    # unsupported decode head dim, and a missing workspace for several splits
+    assert L.hipgpt_attn_decode(p, p, p, p, 1, 1, 8, 48, *([0] * 10), -1.0, 1, None, 0, None) == _lib.ERR_UNSUPPORTED
+    assert L.hipgpt_attn_decode(p, p, p, p, 1, 1, 512, 64, *([0] * 10), -1.0, 4, None, 0, None) == _lib.ERR_WORKSPACE
+    assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 4) == 2 * 3 * 4 * 66 * 4
+    assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 1) == 0
+    assert L.hipgpt_attn_decode_default_splits(64, 12, 2048) >= 2
+
+
+@pytest.mark.parametrize("sym", ["hipgpt_launch_multihead_attention", "_Z26launch_multihead_attentionPKfPfS1_iiii"])
+@pytest.mark.parametrize("E,H", [(63, 2), (64, 0), (64, -1)])
+def test_bad_config_aborts_like_reference(sym, E, H):
+    code = (
+        "import ctypes,sys; L=ctypes.CDLL(sys.argv[1]); f=getattr(L, sys.argv[2]);"
+        "f.argtypes=[ctypes.c_void_p]*3+[ctypes.c_int]*4;"
+        f"f(None,None,None,2,4,{E},{H})"
+    )
+    r = subprocess.run([sys.executable, "-c", code, _lib.LIB_PATH, sym], capture_output=True, text=True)
+    assert r.returncode == -6, r  # SIGABRT
+    assert f"Bad MHA config: E={E} H={H}" in r.stderr
