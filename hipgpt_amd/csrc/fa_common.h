@@ -1,0 +1,103 @@
+// fa_common.h -- pieces shared by the fp32 and bf16 MFMA attention kernels.
+//
+// Both kernels compute the score tile transposed, S^T = K Q^T, with a
+// 32x32 MFMA whose accumulator gives lane l (c = l & 31, h = l >> 5) query
+// column c and the 16 key rows acc_key(r, h), r = 0..15.  A query's row
+// statistics are therefore an in-lane reduction over 16 registers plus one
+// exchange between the two wave halves (v_permlane32_swap), and the
+// exponentiated tile is directly the P^T operand of O^T = V^T P^T.
+#pragma once
+
+#include "common.h"
+
+namespace hipgpt {
+namespace fa {
+
+constexpr int BK = 32;  // keys per tile
+constexpr int QW = 32;  // queries per wave
+
+// Key (within the tile) held by accumulator register r of lane half h.
+__device__ __forceinline__ int acc_key(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// max / sum of x over lanes l and l ^ 32 (the two halves hold the same query).
+__device__ __forceinline__ float halves_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float tile_max(const floatx16& s) {
+    float m = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) m = fmaxf(m, fmaxf(s[r], s[r + 1]));
+    return halves_max(m);
+}
+
+// Mask scores of keys >= Sk and, causally, keys > query + off.
+template <bool CAUSAL>
+__device__ __forceinline__ void mask_tile(floatx16& s, int tb, int hf, int qi, int Sk, int off) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int key = tb + acc_key(r, hf);
+        const bool vis = key < Sk && (!CAUSAL || key <= qi + off);
+        if (!vis) s[r] = kNegInf;
+    }
+}
+
+// Tile loop bounds for a workgroup of NW waves at query block qb.
+struct TileRange {
+    int ntiles;  // tiles the workgroup loads
+    int wtiles;  // tiles this wave computes (a prefix of the above)
+    __device__ __forceinline__ bool edge(int t, int Sk, bool causal, int qw0, int off) const {
+        const int tb = t * BK;
+        return (tb + BK > Sk) || (causal && tb + BK - 1 > qw0 + off);
+    }
+};
+
+template <bool CAUSAL>
+__device__ __forceinline__ TileRange tile_range(int q0, int qw0, int nq_wg, int Sq, int Sk, int off) {
+    TileRange r;
+    int kend = Sk, wkend = Sk;
+    if (CAUSAL) {
+        kend = min(Sk, min(q0 + nq_wg, Sq) + off);
+        wkend = min(Sk, min(qw0 + QW, Sq) + off);
+    }
+    r.ntiles = (kend + BK - 1) / BK;
+    r.wtiles = (qw0 < Sq) ? (wkend + BK - 1) / BK : 0;
+    return r;
+}
+
+// Store a P tile (register r of lane (c, hf) -> probs[qi][tb + acc_key(r, hf)]).
+__device__ __forceinline__ void store_probs_tile(float* prow, const floatx16& p, int tb, int hf, int Sk, bool pvec) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int k0 = tb + 8 * g + 4 * hf;
+        if (pvec && k0 + 3 < Sk) {
+            *reinterpret_cast<floatx4*>(prow + k0) = floatx4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (k0 + j < Sk) prow[k0 + j] = p[4 * g + j];
+        }
+    }
+}
+
+// Causal: zero the probs of this wave's queries for keys >= z0.
+__device__ __forceinline__ void zero_probs_tail(float* probs_bh, int qw0, int Sq, int Sk, int z0, int lane, bool pvec) {
+    for (int r = 0; r < QW; ++r) {
+        const int q = qw0 + r;
+        if (q >= Sq) break;
+        float* pr = probs_bh + (int64_t)q * Sk;
+        if (pvec) {
+            for (int k = z0 + lane * 4; k < Sk; k += 256) *reinterpret_cast<floatx4*>(pr + k) = floatx4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            for (int k = z0 + lane; k < Sk; k += 64) pr[k] = 0.f;
+        }
+    }
+}
+
+}  // namespace fa
+}  // namespace hipgpt
