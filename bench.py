@@ -100,11 +100,12 @@ def time_call(fn, steps, warmup, torch):
     return start.elapsed_time(stop) / steps  # ms per call
 
 
-def cpu_baseline(nthreads):
+def cpu_baseline(nthreads, min_seconds=2.0):
     """The oracle's scalar restatement of the reference kernel HipGPT runs for
     c1 (flash_attention_kernel<32>, causal-restricted) on the whole c1
-    problem, on the host cores."""
-    import numpy as np
+    problem, on the host cores; repeated until min_seconds have elapsed,
+    median time reported."""
+    import statistics
 
     import oracle as O
 
@@ -112,11 +113,14 @@ def cpu_baseline(nthreads):
     E = H * D
     qkv = O.seeded_planar(0x48495047, B, S, E)
     q, k, v = O.planar_qkv(qkv, B, S, E, H)
-    t0 = time.perf_counter()
-    O.attention(q, k, v, causal=True, variant=O.FLASH, nthreads=nthreads)
-    dt = time.perf_counter() - t0
+    times = []
+    while sum(times) < min_seconds or len(times) < 3:
+        t0 = time.perf_counter()
+        O.attention(q, k, v, causal=True, variant=O.FLASH, nthreads=nthreads)
+        times.append(time.perf_counter() - t0)
+    dt = statistics.median(times)
     flops, _ = work(CONFIGS["c1"])
-    return flops / dt, dt, np
+    return flops / dt, dt, len(times)
 
 
 def read_traffic(name):
@@ -134,6 +138,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated config names (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -179,6 +185,16 @@ def main():
         print(f"# {name}: {ms * 1e3:.2f} us  {tflops:.2f} TFLOP/s  {gbs:.0f} GB/s  "
               f"{bound}-bound frac {frac:.3f}", file=sys.stderr, flush=True)
 
+    if args.copy_mb > 0:
+        # A plain copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counters.
+        n = args.copy_mb * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     head = results.get("c1", {})
     line = {
         "metric": METRIC,
@@ -205,13 +221,13 @@ def main():
             "unit": "TFLOP/s", "frac": round(ach / PEAK_F32_MFMA, 4), "traffic": read_traffic("c1"),
         }
     if not args.no_cpu:
-        cpu1, dt1, _ = cpu_baseline(1)
+        cpu1, dt1, n1 = cpu_baseline(1)
         ncores = min(16, os.cpu_count() or 1)
         cpun, dtn, _ = cpu_baseline(ncores)
         line["cpu_baseline"] = {
             "value": round(cpu1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"whole c1 problem (causal, 256 (b,h) pairs) through the scalar restatement of "
-                      f"flash_attention_kernel<32>: {dt1:.2f} s on 1 thread",
+                      f"flash_attention_kernel<32>: median {dt1:.3f} s of {n1} runs on 1 thread",
             "all_cores": {"value": round(cpun / 1e12, 6), "cores": ncores, "seconds": round(dtn, 3)},
         }
     line["configs"] = results
