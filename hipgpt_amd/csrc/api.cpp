@@ -18,6 +18,13 @@ float default_scale(int D, float scale) { return scale > 0.f ? scale : 1.0f / st
 
 int from_hip(hipError_t e) { return e == hipSuccess ? HIPGPT_OK : HIPGPT_ERR_LAUNCH; }
 
+// The MFMA kernels address a (batch, head) slice of K and V with 32-bit byte
+// offsets (buffer loads), including up to a few tiles past the last row.
+bool kv_slice_fits_32bit(const AttnArgs& a, int elem_bytes) {
+    const int64_t ts = a.k_ts > a.v_ts ? a.k_ts : a.v_ts;
+    return ((int64_t)(a.Sk + 256) * ts + a.D) * elem_bytes < ((int64_t)1 << 31);
+}
+
 // Shared validation and dispatch for every forward entry point.
 int attn_dispatch(const AttnArgs& in, int causal, int dtype, hipStream_t stream) {
     if (!in.q || !in.k || !in.v || !in.o) return HIPGPT_ERR_INVALID;
@@ -34,7 +41,7 @@ int attn_dispatch(const AttnArgs& in, int causal, int dtype, hipStream_t stream)
                         a.q_bs % 8 == 0 && a.q_ts % 8 == 0 && a.q_hs % 8 == 0 && a.k_bs % 8 == 0 &&
                         a.k_ts % 8 == 0 && a.k_hs % 8 == 0 && a.v_bs % 8 == 0 && a.v_ts % 8 == 0 &&
                         a.v_hs % 8 == 0 && a.o_bs % 4 == 0 && a.o_ts % 4 == 0 && a.o_hs % 4 == 0;
-        if (!ok) return HIPGPT_ERR_UNSUPPORTED;
+        if (!ok || !kv_slice_fits_32bit(a, 2)) return HIPGPT_ERR_UNSUPPORTED;
         return from_hip(hipgpt::launch_fa_bf16(a, causal != 0, stream));
     }
 
@@ -44,7 +51,7 @@ int attn_dispatch(const AttnArgs& in, int causal, int dtype, hipStream_t stream)
                      (!a.probs || aligned16(a.probs)) && a.q_bs % 4 == 0 && a.q_ts % 4 == 0 &&
                      a.q_hs % 4 == 0 && a.k_bs % 4 == 0 && a.k_ts % 4 == 0 && a.k_hs % 4 == 0 &&
                      a.v_bs % 4 == 0 && a.v_ts % 4 == 0 && a.v_hs % 4 == 0 && a.o_bs % 4 == 0 &&
-                     a.o_ts % 4 == 0 && a.o_hs % 4 == 0;
+                     a.o_ts % 4 == 0 && a.o_hs % 4 == 0 && kv_slice_fits_32bit(a, 4);
     return from_hip(hipgpt::launch_fa_f32(a, causal != 0, vec, stream));
 }
 

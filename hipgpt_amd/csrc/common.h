@@ -21,6 +21,11 @@ constexpr float kMaxInit = -1e30f;
 
 enum Dtype : int { kF32 = 0, kBF16 = 1 };
 
+// Word 3 of a raw (stride 0) buffer resource on CDNA3/CDNA4: 32-bit data
+// format.  Loads past num_records bytes return zero.
+constexpr int kBufferFlags = 0x00020000;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // Strided attention problem as the kernels see it.  Element (b, s, h, d) of
 // a tensor X lives at X[b*x_bs + s*x_ts + h*x_hs + d] (elements of the input
 // dtype).  probs, when not null, is dense fp32 [B][H][Sq][Sk].

@@ -19,32 +19,39 @@ constexpr int QW = 32;  // queries per wave
 // Key (within the tile) held by accumulator register r of lane half h.
 __device__ __forceinline__ int acc_key(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
+// IEEE-754 maximum (NaN-propagating): maps to v_maximum3_f32 on gfx950 and,
+// unlike fmaxf, needs no input canonicalisation.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // max / sum of x over lanes l and l ^ 32 (the two halves hold the same query).
 __device__ __forceinline__ float halves_max(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float halves_sum(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Row max of a score tile: a strict chain, which the compiler folds into
+// eight v_maximum3_f32.
 __device__ __forceinline__ float tile_max(const floatx16& s) {
-    float m = fmaxf(s[0], s[1]);
+    float m = s[0];
 #pragma unroll
-    for (int r = 2; r < 16; r += 2) m = fmaxf(m, fmaxf(s[r], s[r + 1]));
+    for (int r = 1; r < 16; ++r) m = vmax(m, s[r]);
     return halves_max(m);
 }
 
-// Mask scores of keys >= Sk and, causally, keys > query + off.
+// Mask scores of keys >= Sk and, causally, keys > query + off: register r
+// of lane half hf holds key tb + acc_key(r, hf), visible iff
+// acc_key(r, 0) < min(Sk, qi + off + 1) - tb - 4*hf (one compare per score).
 template <bool CAUSAL>
 __device__ __forceinline__ void mask_tile(floatx16& s, int tb, int hf, int qi, int Sk, int off) {
+    int lim = CAUSAL ? min(Sk, qi + off + 1) : Sk;
+    lim -= tb + 4 * hf;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int key = tb + acc_key(r, hf);
-        const bool vis = key < Sk && (!CAUSAL || key <= qi + off);
-        if (!vis) s[r] = kNegInf;
-    }
+    for (int r = 0; r < 16; ++r)
+        if (!(8 * (r >> 2) + (r & 3) < lim)) s[r] = kNegInf;
 }
 
 // Tile loop bounds for a workgroup of NW waves at query block qb.

@@ -1,0 +1,402 @@
+// fa_kernel.h -- the MFMA flash-attention forward kernel body, shared by the
+// fp32 (fa_f32.hip) and bf16 (fa_bf16.hip) instantiations through a traits
+// type that supplies the operand layouts and the two matrix products.
+//
+// Work decomposition (one workgroup = NQS x NKS waves):
+//   * The workgroup owns NQS*32 consecutive queries of one (batch, head).
+//     Wave (qs, ks) owns the 32 queries of sub-block qs and every NKS-th
+//     key tile starting at tile ks, so a long causal row is split over NKS
+//     waves (balance) and the CU holds NKS times more waves (latency hiding).
+//   * One stage = NKS key tiles of 32 rows, staged global -> registers ->
+//     LDS (K row-major, V transposed), double buffered, one barrier per
+//     stage; the next stage's global loads are in flight during compute.
+//   * Per tile: S^T = K Q^T (32x32 MFMA accumulator, layout in fa_common.h),
+//     mask, online softmax in the log2 domain, O^T += V^T P^T with P taken
+//     straight from the accumulator registers.
+//   * The NKS partial states (m, l, O) of a query sub-block are merged in
+//     LDS at the end (log-sum-exp), or, when probs are written, the row
+//     max/sum are merged after sweep 1 and the already normalised partial O
+//     are summed after sweep 2.
+//   * Causal: tiles above a wave's diagonal are skipped (wave-uniform), only
+//     diagonal tiles are masked, query blocks are launched longest-first.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "fa_common.h"
+
+namespace hipgpt {
+namespace fa {
+
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+struct FaKernel {
+    static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");
+    static constexpr int DP = TR::DP;
+    static constexpr int NW = NQS * NKS;
+    static constexpr int NT = NW * 64;
+    static constexpr int NDB = DP / 32;
+    using E = typename TR::elem;
+
+    // LDS: two stage buffers of NKS (K tile + V^T tile); the end-of-kernel
+    // merge reuses the same memory.
+    static constexpr int STAGE_ELEMS = NKS * (TR::KTILE + TR::VTILE);
+    static constexpr int STAGE_BYTES = STAGE_ELEMS * (int)sizeof(E);
+    static constexpr int MERGE_BYTES = NW * 64 * (16 * NDB + 2) * 4;
+    static constexpr int LDS_BYTES = (2 * STAGE_BYTES > MERGE_BYTES) ? 2 * STAGE_BYTES : MERGE_BYTES;
+
+    // Global -> register staging of one stage (K and V), 16-byte chunks.
+    static constexpr int EPC = 16 / (int)sizeof(E);      // elements per chunk
+    static constexpr int CPR = DP / EPC;                  // chunks per row
+    static constexpr int CPS = NKS * BK * CPR;            // chunks per stage (K or V)
+    static constexpr int PER = (CPS + NT - 1) / NT;
+
+    // 16-byte loads go through buffer resources whose range is the (b, h)
+    // slice's valid K / V rows: rows past Sk read as zero without a
+    // predicate, and each load costs one 32-bit offset add.  (Non-VEC
+    // problems -- D below the padded dim or unaligned strides -- use plain
+    // guarded loads.)
+    struct Stager {
+        typename TR::chunk kr[PF][PER], vr[PF][PER];  // PF register slots of one stage each
+        int koff[PER], voff[PER];  // byte offsets of this thread's chunks from the stage's first row
+        __amdgpu_buffer_rsrc_t krs, vrs;
+        int kstage, vstage;        // bytes per stage of NKS*BK rows
+        const E *Kp, *Vp;
+        int64_t kts, vts;
+        int Sk, D;
+
+        __device__ __forceinline__ void init(const E* Kp_, const E* Vp_, int64_t kts_, int64_t vts_, int Sk_, int D_,
+                                             int tid) {
+            Kp = Kp_;
+            Vp = Vp_;
+            kts = kts_;
+            vts = vts_;
+            Sk = Sk_;
+            D = D_;
+            if (VEC) {
+                constexpr int ES = (int)sizeof(E);
+                krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<E*>(Kp), 0,
+                                                        (int)(((int64_t)(Sk - 1) * kts + D) * ES), kBufferFlags);
+                vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<E*>(Vp), 0,
+                                                        (int)(((int64_t)(Sk - 1) * vts + D) * ES), kBufferFlags);
+                kstage = (int)(NKS * BK * kts * ES);
+                vstage = (int)(NKS * BK * vts * ES);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    const int f = tid + i * NT;
+                    const int row = f / CPR;
+                    const int cc = f % CPR;
+                    koff[i] = (int)((row * kts + cc * EPC) * ES);
+                    voff[i] = (int)((row * vts + cc * EPC) * ES);
+                }
+            }
+        }
+
+        template <int SL>
+        __device__ __forceinline__ void load(int stage, int tid) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if (VEC) {
+                    if (CPS % NT == 0 || f < CPS) {
+                        kr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
+                        vr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
+                    }
+                } else {
+                    const int row = f / CPR;  // 0 .. NKS*BK-1
+                    const int cc = f % CPR;
+                    const int key = stage * NKS * BK + row;
+                    const bool ok = (CPS % NT == 0 || f < CPS) && key < Sk;
+                    kr[SL][i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
+                    vr[SL][i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
+                }
+            }
+        }
+        template <int SL>
+        __device__ __forceinline__ void store(E* stage, int tid) const {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if (CPS % NT != 0 && f >= CPS) break;
+                const int row = f / CPR;
+                const int cc = f % CPR;
+                const int kt = row / BK;  // tile within the stage
+                const int r = row % BK;
+                E* Kt = stage + kt * TR::KTILE;
+                E* Vt = stage + NKS * TR::KTILE + kt * TR::VTILE;
+                TR::store_k_chunk(Kt, r, cc, kr[SL][i]);
+                TR::store_vt_chunk(Vt, r, cc, vr[SL][i]);
+            }
+        }
+    };
+
+    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw) {
+        E* const lds = reinterpret_cast<E*>(lds_raw);
+        const int tid = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+        const int c = lane & 31;
+        const int hf = lane >> 5;
+        const int BH = a.B * a.H;
+        const int bh = blockIdx.x % BH;
+        const int rank = blockIdx.x / BH;
+        const int qb = CAUSAL ? a.n_qblk - 1 - rank : rank;  // longest rows first
+        // Wave w runs on SIMD w % 4.  Rotating the wave -> (sub-block, split)
+        // roles with the launch rank gives each SIMD a different role in
+        // each of the co-resident workgroups, evening out causal work.
+        const int role = (wave + rank) % NW;
+        const int qs = role / NKS;
+        const int ks = role % NKS;
+        const int b = bh / a.H;
+        const int h = bh % a.H;
+
+        const int q0 = qb * (NQS * QW);
+        const int qw0 = q0 + qs * QW;
+        const int qi = qw0 + c;
+        const int Sq = a.Sq, Sk = a.Sk, off = a.causal_off;
+
+        const E* Qp = static_cast<const E*>(a.q) + b * a.q_bs + h * a.q_hs;
+        const E* Kp = static_cast<const E*>(a.k) + b * a.k_bs + h * a.k_hs;
+        const E* Vp = static_cast<const E*>(a.v) + b * a.v_bs + h * a.v_hs;
+
+        const TileRange tr = tile_range<CAUSAL>(q0, qw0, NQS * QW, Sq, Sk, off);
+        const int nstages = (tr.ntiles + NKS - 1) / NKS;
+        const int wtiles = tr.wtiles;
+
+        typename TR::QReg qreg;
+        TR::template load_q<VEC>(qreg, Qp + (int64_t)qi * a.q_ts, hf, qi < Sq, a.D, a.qscale);
+        const float sc = TR::score_scale(a.qscale);
+
+        floatx16 o[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+
+        float m_run = kMaxInit;
+        float l_run = 0.f;
+
+        auto tile_scores = [&](const E* stage, int t) -> floatx16 {
+            floatx16 s = TR::qk(stage + (t % NKS) * TR::KTILE, qreg, c, hf);
+            if (tr.edge(t, Sk, CAUSAL, qw0, off)) mask_tile<CAUSAL>(s, t * BK, hf, qi, Sk, off);
+            return s;
+        };
+        auto vt_of = [&](const E* stage, int t) -> const E* {
+            return stage + NKS * TR::KTILE + (t % NKS) * TR::VTILE;
+        };
+
+        Stager st;
+        st.init(Kp, Vp, a.k_ts, a.v_ts, Sk, a.D, tid);
+        // ------------------------------------------------------------------
+        // Stage loop.  MODE 0: online softmax + PV.  MODE 1: max/sum only.
+        // MODE 2: probs store + PV with the final (m, l).
+        // One stage of compute on LDS buffer (i & 1).  MODE 0: online softmax
+        // + PV.  MODE 1: max/sum only.  MODE 2: probs store + PV with the
+        // final (m, l).
+        auto compute = [&](auto mode_tag, int i, float linv, float* prow, bool pvec) {
+            constexpr int MODE = decltype(mode_tag)::value;
+            const E* cur = lds + (i & 1) * STAGE_ELEMS;
+            const int t = i * NKS + ks;
+            if (t >= wtiles) return;
+            floatx16 s = tile_scores(cur, t);
+            typename TR::VReg vreg;
+            if (MODE != 1) TR::load_v(vreg, vt_of(cur, t), c, hf);  // in flight during the softmax
+            if (MODE == 0) {
+                const float m_new = vmax(m_run, tile_max(s) * sc);
+                float ls = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    s[r] = fast_exp2(fmaf(s[r], sc, -m_new));
+                    ls += s[r];
+                }
+                ls = halves_sum(ls);
+                if (__any(m_new != m_run)) {  // rescale only when a row max moved
+                    const float alpha = fast_exp2(m_run - m_new);
+                    l_run *= alpha;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                }
+                l_run += ls;
+                m_run = m_new;
+                TR::pv(vreg, s, o, c, hf);
+            } else if (MODE == 1) {
+                const float m_new = vmax(m_run, tile_max(s) * sc);
+                float ls = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(s[r], sc, -m_new));
+                l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
+                m_run = m_new;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -m_run)) * linv;
+                if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
+                TR::pv(vreg, s, o, c, hf);
+            }
+        };
+
+        // Stage pipeline.  PF = 1: stage i+1 is loaded into registers while
+        // stage i is computed.  PF = 2: two register slots; stage i+2 is
+        // requested while stage i is computed and stage i+1 (requested one
+        // stage earlier) is written to LDS afterwards, so every global load
+        // has two stages of compute to land.
+        auto sweep = [&](auto mode_tag, float linv, float* prow, bool pvec) {
+            if (nstages > 0) {
+                st.template load<0>(0, tid);
+                if (PF == 2 && nstages > 1) st.template load<PF - 1>(1, tid);
+                st.template store<0>(lds, tid);
+            }
+            __syncthreads();
+            auto iter = [&](int i, auto slot_tag) {
+                constexpr int SL = decltype(slot_tag)::value;  // slot free for new loads
+                constexpr int NX = PF == 2 ? 1 - SL : 0;      // slot holding stage i+1
+                if (i + PF < nstages) st.template load<SL>(i + PF, tid);
+                compute(mode_tag, i, linv, prow, pvec);
+                if (i + 1 < nstages) st.template store<NX>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                __syncthreads();
+            };
+            for (int i = 0; i < nstages; i += PF) {
+                iter(i, std::integral_constant<int, 0>{});
+                if (PF == 2 && i + 1 < nstages) iter(i + 1, std::integral_constant<int, PF - 1>{});
+            }
+        };
+
+        float* const mrg = reinterpret_cast<float*>(lds_raw);  // merge scratch (after a barrier)
+        float* const m_slot = mrg;                              // [NW][64]
+        float* const l_slot = mrg + NW * 64;                    // [NW][64]
+        float* const o_slot = mrg + 2 * NW * 64;                // [NW][16*NDB][64]
+
+        if (!PROBS) {
+            sweep(std::integral_constant<int, 0>{}, 0.f, nullptr, false);
+            if (NKS > 1) {
+                // wave ks > 0 publishes (m, l, O); wave ks == 0 merges
+                if (ks != 0) {
+                    m_slot[role * 64 + lane] = m_run;
+                    l_slot[role * 64 + lane] = l_run;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o_slot[(role * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
+                }
+                __syncthreads();
+                if (ks == 0) {
+                    float M = m_run;
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j) M = fmaxf(M, m_slot[(role + j) * 64 + lane]);
+                    const float w0 = fast_exp2(m_run - M);
+                    l_run *= w0;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[db][r] *= w0;
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j) {
+                        const float wj = fast_exp2(m_slot[(role + j) * 64 + lane] - M);
+                        l_run = fmaf(l_slot[(role + j) * 64 + lane], wj, l_run);
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                o[db][r] = fmaf(o_slot[((role + j) * 16 * NDB + db * 16 + r) * 64 + lane], wj, o[db][r]);
+                    }
+                }
+            }
+        } else {
+            sweep(std::integral_constant<int, 1>{}, 0.f, nullptr, false);
+            if (NKS > 1) {
+                m_slot[role * 64 + lane] = m_run;
+                l_slot[role * 64 + lane] = l_run;
+                __syncthreads();
+                const int w0 = qs * NKS;
+                float M = kMaxInit;
+#pragma unroll
+                for (int j = 0; j < NKS; ++j) M = fmaxf(M, m_slot[(w0 + j) * 64 + lane]);
+                float L = 0.f;
+#pragma unroll
+                for (int j = 0; j < NKS; ++j) L = fmaf(l_slot[(w0 + j) * 64 + lane], fast_exp2(m_slot[(w0 + j) * 64 + lane] - M), L);
+                m_run = M;
+                l_run = L;
+                __syncthreads();  // the stage buffers overwrite the slots next
+            }
+            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
+            const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
+            sweep(std::integral_constant<int, 2>{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
+            if (CAUSAL && qw0 < Sq && ks == 0) {
+                const int ztile = tr.wtiles;  // tiles [0, wtiles) were written by the NKS waves
+                zero_probs_tail(probs_bh, qw0, Sq, Sk, ztile * BK, lane, pvec);
+            }
+            if (NKS > 1) {
+                if (ks != 0) {
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o_slot[(role * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
+                }
+                __syncthreads();
+                if (ks == 0) {
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j)
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) o[db][r] += o_slot[((role + j) * 16 * NDB + db * 16 + r) * 64 + lane];
+                }
+            }
+            l_run = 1.0f;
+        }
+
+        // ---------------- epilogue: O = O^T / l (wave ks == 0) ----------------
+        if (ks == 0 && qi < Sq) {
+            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d0 = db * 32 + 8 * g + 4 * hf;
+                    const floatx4 v = {o[db][4 * g] * linv, o[db][4 * g + 1] * linv, o[db][4 * g + 2] * linv,
+                                       o[db][4 * g + 3] * linv};
+                    if (VEC) {
+                        *reinterpret_cast<floatx4*>(orow + d0) = v;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (d0 + j < a.D) orow[d0 + j] = v[j];
+                    }
+                }
+            }
+        }
+    }
+};
+
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+__global__ __launch_bounds__(NQS* NKS * 64) void fa_fwd_kernel(AttnArgs a) {
+    using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[K::LDS_BYTES];
+    K::run(a, lds);
+}
+
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
+    AttnArgs args = a;
+    args.n_qblk = (a.Sq + NQS * QW - 1) / (NQS * QW);
+    const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>), dim3((unsigned)grid),
+                       dim3(NQS * NKS * 64), 0, stream, args);
+    return hipGetLastError();
+}
+
+template <class TR, int NQS, int NKS, int PF, bool VEC>
+hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
+    if (causal)
+        return probs ? launch_fa<TR, NQS, NKS, PF, true, true, VEC>(a, s)
+                     : launch_fa<TR, NQS, NKS, PF, true, false, VEC>(a, s);
+    return probs ? launch_fa<TR, NQS, NKS, PF, false, true, VEC>(a, s)
+                 : launch_fa<TR, NQS, NKS, PF, false, false, VEC>(a, s);
+}
+
+}  // namespace fa
+}  // namespace hipgpt
