@@ -19,6 +19,7 @@
 //   D[m][n]: register r holds D[8*(r/4) + 4*h + (r%4)][c]
 #include "common.h"
 #include "fa_kernel.h"
+#include "fa_resident.h"
 #include "kernels.h"
 
 namespace hipgpt {
@@ -190,8 +191,28 @@ int fa_f32_padded_dim(int D) {
     return 0;
 }
 
+// Short sequences at DP = 64 (all K/V tiles of a (b, h) fit one workgroup's
+// LDS) run the resident kernel: 8 waves = 256 queries per workgroup.  At
+// DP = 32 the streaming kernel measured faster (its four waves per SIMD hide
+// the short tiles' softmax better), so the resident path is off there unless
+// HIPGPT_RES_D32_NKS is set to 1 or 2 at build time.
+#ifndef HIPGPT_RESIDENT_MAX_SQ
+#define HIPGPT_RESIDENT_MAX_SQ 256
+#endif
+#ifndef HIPGPT_RES_D32_NKS
+#define HIPGPT_RES_D32_NKS 0
+#endif
+
 hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t stream) {
     const bool probs = a.probs != nullptr;
+    if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ) {
+#if HIPGPT_RES_D32_NKS > 0
+        if (a.D == 32 && fa::resident_lds_bytes<F32Traits<32>, 8, HIPGPT_RES_D32_NKS>(a) != 0)
+            return fa::launch_resident<F32Traits<32>, 8, HIPGPT_RES_D32_NKS, 4>(a, causal, stream);
+#endif
+        if (a.D == 64 && fa::resident_lds_bytes<F32Traits<64>, 8, 1>(a) != 0)
+            return fa::launch_resident<F32Traits<64>, 8, 1, 4>(a, causal, stream);
+    }
     switch (fa_f32_padded_dim(a.D)) {
         case 32:
             return launch_dp<32, HIPGPT_F32_D32_NQS, HIPGPT_F32_D32_NKS, HIPGPT_F32_D32_PF>(a, causal, probs, vec, stream);

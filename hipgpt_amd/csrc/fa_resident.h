@@ -1,0 +1,395 @@
+// fa_resident.h -- attention forward with the whole K/V of a (batch, head)
+// resident in LDS, for short sequences (HipGPT's default S = 256).
+//
+// At S = 256 the streaming kernel (fa_kernel.h) spends a large share of its
+// time in the prologue (every workgroup loads Q and its first stage at once)
+// and in per-stage barriers that keep waves with unequal causal work in
+// lockstep.  Here one workgroup of NQS x NKS waves owns NQS*32 queries of one
+// (b, h) and keeps every K tile (row-major) and V^T tile it needs in LDS:
+//   * Production: tile t is split over all threads; each thread keeps L
+//     tiles of loads in flight in registers, writes its share of tile t to
+//     LDS, and the wave then bumps an LDS arrival counter for t.
+//   * Consumption: a wave that needs tile t waits until all NW waves have
+//     signalled it (bounded spin), then computes it.  Every wave produces
+//     tile t before it waits on tile t, so the wait always ends; there is no
+//     workgroup barrier after the first, so waves with little causal work
+//     finish early instead of idling in lockstep.
+//   * Balance: wave w runs on SIMD w % 4.  The waves of SIMD s take query
+//     sub-blocks s and NQS-1-s (NQS = 8), and with NKS = 2 each sub-block's
+//     tiles alternate between two waves, so every SIMD carries the same
+//     causal work; the NKS partial (m, l, O) are merged in LDS at the end.
+//   * With probs the second sweep re-reads K/V from LDS (no reload).
+// The per-tile math (S^T = K Q^T, mask, online softmax, O^T += V^T P^T) is the
+// same as the streaming kernel's, through the same operand traits.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "fa_common.h"
+
+namespace hipgpt {
+namespace fa {
+
+// Largest LDS footprint a resident workgroup may use (bytes).
+constexpr int kResidentLdsMax = 152 * 1024;
+
+template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
+struct FaResident {
+    static_assert(NQS == 8 && (NKS == 1 || NKS == 2), "8 sub-blocks, one or two key splits");
+    static constexpr int NW = NQS * NKS;
+    static constexpr int DP = TR::DP;
+    static constexpr int NT = NW * 64;
+    static constexpr int NDB = DP / 32;
+    using E = typename TR::elem;
+    static constexpr int TILE_ELEMS = TR::KTILE + TR::VTILE;
+    static constexpr int EPC = 16 / (int)sizeof(E);
+    static constexpr int CPR = DP / EPC;                 // 16-byte chunks per row
+    static constexpr int CPT = BK * CPR;                 // chunks per tile, K (same for V)
+    static constexpr int PER = (2 * CPT + NT - 1) / NT;  // K+V chunks per thread per tile
+
+    // LDS layout: [0, 256) arrival counters; [256, 256 + ML_BYTES) per-wave
+    // (m, l) for the probs sweep merge; then the tiles.  The final O merge
+    // reuses the tile area (after a barrier).
+    static constexpr int ML_BYTES = NKS > 1 ? NW * 64 * 2 * 4 : 0;
+    static constexpr int HEAD_BYTES = 256 + ML_BYTES;
+    static constexpr int MERGE_BYTES = NKS > 1 ? NW * 64 * 16 * NDB * 4 : 0;
+
+    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max) {
+        E* const tiles = reinterpret_cast<E*>(lds_raw + HEAD_BYTES);
+        int* const cnt = reinterpret_cast<int*>(lds_raw);  // 64 arrival counters
+
+        const int tid = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = tid >> 6;
+        const int c = lane & 31;
+        const int hf = lane >> 5;
+
+        const int BH = a.B * a.H;
+        const int bh = blockIdx.x % BH;
+        const int rank = blockIdx.x / BH;
+        const int qb = CAUSAL ? a.n_qblk - 1 - rank : rank;
+        const int b = bh / a.H;
+        const int h = bh % a.H;
+        // Waves s, s+4, s+8, s+12 share SIMD s: sub-blocks s and NQS-1-s, key
+        // splits 0 and 1.
+        const int simd = wave & 3, grp = wave >> 2;
+        const int sub = (grp & 1) ? NQS - 1 - simd : simd;
+        const int ks = grp >> 1;
+        const int slot = sub * NKS + ks;
+
+        const int q0 = qb * (NQS * QW);
+        const int qw0 = q0 + sub * QW;
+        const int qi = qw0 + c;
+        const int Sq = a.Sq, Sk = a.Sk, off = a.causal_off;
+
+        const E* Qp = static_cast<const E*>(a.q) + b * a.q_bs + h * a.q_hs;
+        const E* Kp = static_cast<const E*>(a.k) + b * a.k_bs + h * a.k_hs;
+        const E* Vp = static_cast<const E*>(a.v) + b * a.v_bs + h * a.v_hs;
+
+        const TileRange tr = tile_range<CAUSAL>(q0, qw0, NQS * QW, Sq, Sk, off);
+        const int T = min(tr.ntiles, ntiles_max);  // host guarantees ntiles <= ntiles_max
+        const int wtiles = tr.wtiles;
+
+        if (tid < 64) cnt[tid] = 0;
+        __syncthreads();
+
+        // ---- producer state: this thread's chunks of every tile ----
+        constexpr int ES = (int)sizeof(E);
+        const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<E*>(Kp), 0, (int)(((int64_t)(Sk - 1) * a.k_ts + a.D) * ES), kBufferFlags);
+        const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<E*>(Vp), 0, (int)(((int64_t)(Sk - 1) * a.v_ts + a.D) * ES), kBufferFlags);
+        const int ktile = (int)(BK * a.k_ts * ES);
+        const int vtile = (int)(BK * a.v_ts * ES);
+        int goff[PER];  // byte offset within tile 0 (K or V)
+        bool isv[PER], act[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * NT;
+            act[i] = (2 * CPT) % NT == 0 || f < 2 * CPT;
+            isv[i] = f >= CPT;
+            const int g = isv[i] ? f - CPT : f;
+            const int row = g / CPR, cc = g % CPR;
+            goff[i] = (int)((row * (isv[i] ? a.v_ts : a.k_ts) + cc * EPC) * ES);
+        }
+        typename TR::chunk ring[L][PER];
+        auto issue = [&](int t, auto slot_tag) {
+            constexpr int SL = decltype(slot_tag)::value;
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if (act[i])
+                    ring[SL][i] = TR::from_u32x4(isv[i] ? __builtin_amdgcn_raw_buffer_load_b128(vrs, goff[i] + t * vtile, 0, 0)
+                                                        : __builtin_amdgcn_raw_buffer_load_b128(krs, goff[i] + t * ktile, 0, 0));
+        };
+        auto publish = [&](int t, auto slot_tag) {
+            constexpr int SL = decltype(slot_tag)::value;
+            E* Kt = tiles + t * TILE_ELEMS;
+            E* Vt = Kt + TR::KTILE;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                if (!act[i]) continue;
+                const int f = tid + i * NT;
+                const int g = isv[i] ? f - CPT : f;
+                const int row = g / CPR, cc = g % CPR;
+                if (isv[i])
+                    TR::store_vt_chunk(Vt, row, cc, ring[SL][i]);
+                else
+                    TR::store_k_chunk(Kt, row, cc, ring[SL][i]);
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+            if (lane == 0) __hip_atomic_fetch_add(&cnt[t], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        auto wait_tile = [&](int t) {
+            // Bounded: every wave signals every tile before waiting on it.
+            for (int spin = 0; spin < (1 << 22); ++spin) {
+                if (__hip_atomic_load(&cnt[t], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+        };
+
+        // ---- consumer state ----
+        typename TR::QReg qreg;
+        TR::template load_q<true>(qreg, Qp + (int64_t)qi * a.q_ts, hf, qi < Sq, a.D, a.qscale);
+        const float sc = TR::score_scale(a.qscale);
+        floatx16 o[NDB];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+        float m_run = kMaxInit, l_run = 0.f;
+
+        auto scores = [&](int t) -> floatx16 {
+            floatx16 s = TR::qk(tiles + t * TILE_ELEMS, qreg, c, hf);
+            if (tr.edge(t, Sk, CAUSAL, qw0, off)) mask_tile<CAUSAL>(s, t * BK, hf, qi, Sk, off);
+            return s;
+        };
+        auto online = [&](int t) {
+            floatx16 s = scores(t);
+            typename TR::VReg vreg;
+            TR::load_v(vreg, tiles + t * TILE_ELEMS + TR::KTILE, c, hf);
+            const float m_new = vmax(m_run, tile_max(s) * sc);
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(fmaf(s[r], sc, -m_new));
+                ls += s[r];
+            }
+            ls = halves_sum(ls);
+            if (__any(m_new != m_run)) {
+                const float alpha = fast_exp2(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            }
+            l_run += ls;
+            m_run = m_new;
+            TR::pv(vreg, s, o, c, hf);
+        };
+        auto stats = [&](int t) {
+            const floatx16 s = scores(t);
+            const float m_new = vmax(m_run, tile_max(s) * sc);
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(s[r], sc, -m_new));
+            l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
+            m_run = m_new;
+        };
+
+        // ---- produce every tile, consume the ones this wave needs ----
+        // Production runs L tiles ahead of consumption: tiles 0..L-1 are
+        // published before any compute, then tile t+L is published (and
+        // t+2L requested) before tile t is computed.  Slot of tile t: t % L
+        // (compile-time: the loops are unrolled L times).
+        static_assert(L == 2 || L == 4, "ring depth");
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, (L == 4 ? 2 : 0)>;
+        using S3 = std::integral_constant<int, (L == 4 ? 3 : 1)>;
+        auto ahead = [&](int t, auto slot_tag) {  // initial run-ahead for tile t < L
+            if (t < T) {
+                publish(t, slot_tag);
+                if (t + L < T) issue(t + L, slot_tag);
+            }
+        };
+        auto step = [&](int t, auto slot_tag) {
+            if (t >= T) return;
+            if (t + L < T) {
+                publish(t + L, slot_tag);
+                if (t + 2 * L < T) issue(t + 2 * L, slot_tag);
+            }
+            if (t < wtiles && t % NKS == ks) {
+                wait_tile(t);
+                if (PROBS)
+                    stats(t);
+                else
+                    online(t);
+            }
+        };
+        if (0 < T) issue(0, S0{});
+        if (1 < T) issue(1, S1{});
+        if (L == 4) {
+            if (2 < T) issue(2, S2{});
+            if (3 < T) issue(3, S3{});
+        }
+        ahead(0, S0{});
+        ahead(1, S1{});
+        if (L == 4) {
+            ahead(2, S2{});
+            ahead(3, S3{});
+        }
+        for (int t0 = 0; t0 < T; t0 += L) {
+            step(t0, S0{});
+            step(t0 + 1, S1{});
+            if (L == 4) {
+                step(t0 + 2, S2{});
+                step(t0 + 3, S3{});
+            }
+        }
+
+        float* const ml = reinterpret_cast<float*>(lds_raw + 256);  // [NW][2][64]
+        if (PROBS) {
+            if (NKS > 1) {  // combine the splits' (m, l): every split needs the row's final values
+                ml[(slot * 2) * 64 + lane] = m_run;
+                ml[(slot * 2 + 1) * 64 + lane] = l_run;
+                __syncthreads();
+                float M = kMaxInit, L2 = 0.f;
+#pragma unroll
+                for (int j = 0; j < NKS; ++j) M = fmaxf(M, ml[((sub * NKS + j) * 2) * 64 + lane]);
+#pragma unroll
+                for (int j = 0; j < NKS; ++j)
+                    L2 = fmaf(ml[((sub * NKS + j) * 2 + 1) * 64 + lane], fast_exp2(ml[((sub * NKS + j) * 2) * 64 + lane] - M), L2);
+                m_run = M;
+                l_run = L2;
+            }
+            // sweep 2 from the resident tiles: P = exp(s - m) / l stored once, P V
+            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
+            float* prow = probs_bh + (int64_t)qi * Sk;
+            const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
+            for (int t = ks; t < wtiles; t += NKS) {
+                floatx16 s = scores(t);
+                typename TR::VReg vreg;
+                TR::load_v(vreg, tiles + t * TILE_ELEMS + TR::KTILE, c, hf);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -m_run)) * linv;
+                if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
+                TR::pv(vreg, s, o, c, hf);
+            }
+            if (CAUSAL && qw0 < Sq && ks == 0) zero_probs_tail(probs_bh, qw0, Sq, Sk, wtiles * BK, lane, pvec);
+            l_run = 1.0f;
+        }
+
+        if (NKS > 1) {
+            // merge the key splits of each sub-block through the (now idle) tile area
+            float* const mo = reinterpret_cast<float*>(tiles);  // [NW][16*NDB][64]
+            __syncthreads();
+            if (ks != 0) {
+                ml[(slot * 2) * 64 + lane] = m_run;
+                ml[(slot * 2 + 1) * 64 + lane] = l_run;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mo[(slot * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
+            }
+            __syncthreads();
+            if (ks == 0) {
+                if (PROBS) {  // partial O are already normalised: sum them
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j)
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) o[db][r] += mo[((slot + j) * 16 * NDB + db * 16 + r) * 64 + lane];
+                } else {
+                    float M = m_run;
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j) M = fmaxf(M, ml[((slot + j) * 2) * 64 + lane]);
+                    const float w0 = fast_exp2(m_run - M);
+                    l_run *= w0;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) o[db][r] *= w0;
+#pragma unroll
+                    for (int j = 1; j < NKS; ++j) {
+                        const float wj = fast_exp2(ml[((slot + j) * 2) * 64 + lane] - M);
+                        l_run = fmaf(ml[((slot + j) * 2 + 1) * 64 + lane], wj, l_run);
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                o[db][r] = fmaf(mo[((slot + j) * 16 * NDB + db * 16 + r) * 64 + lane], wj, o[db][r]);
+                    }
+                }
+            }
+        }
+
+        if (ks == 0 && qi < Sq) {
+            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<floatx4*>(orow + db * 32 + 8 * g + 4 * hf) =
+                        floatx4{o[db][4 * g] * linv, o[db][4 * g + 1] * linv, o[db][4 * g + 2] * linv,
+                                o[db][4 * g + 3] * linv};
+        }
+    }
+};
+
+template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
+__global__ __launch_bounds__(NQS* NKS * 64) void fa_resident_kernel(AttnArgs a, int ntiles_max) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_dyn[];
+    FaResident<TR, NQS, NKS, L, CAUSAL, PROBS>::run(a, lds_dyn, ntiles_max);
+}
+
+// Dynamic-LDS bytes for a resident launch over all ceil(Sk / 32) key tiles
+// (the last query block of a causal problem sees every key), or 0 when the
+// problem does not fit one workgroup's LDS.
+template <class TR, int NQS, int NKS>
+inline size_t resident_lds_bytes(const AttnArgs& a) {
+    using R = FaResident<TR, NQS, NKS, 4, false, false>;
+    const int64_t tiles = ((int64_t)a.Sk + BK - 1) / BK;
+    int64_t body = tiles * R::TILE_ELEMS * (int64_t)sizeof(typename TR::elem);
+    if (body < R::MERGE_BYTES) body = R::MERGE_BYTES;
+    const int64_t bytes = R::HEAD_BYTES + body;
+    return (tiles <= 64 && bytes <= kResidentLdsMax) ? (size_t)bytes : 0;
+}
+
+template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
+hipError_t launch_resident_one(const AttnArgs& args, int ntiles, size_t lds, int64_t grid, hipStream_t stream) {
+    auto kern = fa_resident_kernel<TR, NQS, NKS, L, CAUSAL, PROBS>;
+    static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLdsMax);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), lds, stream, args, ntiles);
+    return hipGetLastError();
+}
+
+template <class TR, int NQS, int NKS, int L>
+hipError_t launch_resident(const AttnArgs& a, bool causal, hipStream_t stream) {
+    const size_t lds = resident_lds_bytes<TR, NQS, NKS>(a);
+    if (lds == 0) return hipErrorInvalidConfiguration;
+    const int ntiles = (a.Sk + BK - 1) / BK;
+    AttnArgs args = a;
+    args.n_qblk = (a.Sq + NQS * QW - 1) / (NQS * QW);
+    const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    const bool probs = a.probs != nullptr;
+    if (causal)
+        return probs ? launch_resident_one<TR, NQS, NKS, L, true, true>(args, ntiles, lds, grid, stream)
+                     : launch_resident_one<TR, NQS, NKS, L, true, false>(args, ntiles, lds, grid, stream);
+    return probs ? launch_resident_one<TR, NQS, NKS, L, false, true>(args, ntiles, lds, grid, stream)
+                 : launch_resident_one<TR, NQS, NKS, L, false, false>(args, ntiles, lds, grid, stream);
+}
+
+}  // namespace fa
+}  // namespace hipgpt
