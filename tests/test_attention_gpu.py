@@ -102,7 +102,8 @@ def test_legacy_matches_reference_hip_kernels(dev, B, S, E, H):
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("B,Sq,Sk,H,D", [(2, 40, 40, 3, 64), (1, 17, 90, 2, 32), (2, 64, 200, 2, 128),
-                                         (1, 33, 33, 2, 48), (1, 3, 70, 2, 256)])
+                                         (1, 33, 33, 2, 48), (1, 3, 70, 2, 256), (1, 20, 150, 2, 64),
+                                         (2, 200, 256, 2, 64)])
 def test_strided_interleaved_layout(dev, B, Sq, Sk, H, D, causal):
     """q, k, v as views into the caller's row-interleaved [T, 3E] buffer
     (src/transformer_layer.cpp:217) -- the layout the stride-aware API takes
