@@ -35,6 +35,11 @@ CONFIGS = {
     "c3_bf16": (8, 12, 1024, 1024, 64, True, "bf16", False, "fwd"),
     "c4": (4, 16, 2048, 2048, 128, True, "f32", False, "fwd"),
     "c5": (64, 12, 1, 2048, 64, False, "f32", False, "decode"),
+    # HipGPT's unfused single-head helpers (include/hip_kernels.h:44-46) at the
+    # c1 shape with batch and heads merged (B*H = 256 sequences of 256 x 32).
+    "a8_scores": (256, 1, 256, 256, 32, False, "f32", False, "sdp"),
+    "a8_softmax": (256, 1, 256, 256, 32, False, "f32", False, "softmax"),
+    "a8_wsum": (256, 1, 256, 256, 32, False, "f32", False, "wsum"),
 }
 
 
@@ -42,6 +47,12 @@ def work(cfg):
     """Algorithmic FLOPs (4*B*H*D*P, P visible pairs) and HBM bytes (Q, K, V
     read once, O written once, plus probs when written)."""
     B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+    if kind == "sdp":  # read Q, K; write scores
+        return 2.0 * B * Sq * Sk * D, 4 * (2 * B * Sq * D + B * Sq * Sk)
+    if kind == "softmax":  # read and write B*S*S (no flops counted)
+        return 0.0, 8 * B * Sq * Sk
+    if kind == "wsum":  # read P, V; write O
+        return 2.0 * B * Sq * Sk * D, 4 * (B * Sq * Sk + 2 * B * Sq * D)
     if kind == "decode":
         pairs = Sk
     elif causal:
@@ -70,6 +81,17 @@ def make_call(cfg, torch, A, dev):
         ns = A.decode_default_splits(B, H, Sk)
         ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
         return lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws), {"splits": ns}
+    if kind in ("sdp", "softmax", "wsum"):
+        x = torch.randn(3, B * Sq, D, device=dev, generator=g)
+        sc = torch.randn(B * Sq, Sk, device=dev, generator=g)
+        out = torch.empty(B * Sq, Sk, device=dev)
+        o = torch.empty(B * Sq, D, device=dev)
+        if kind == "sdp":
+            return lambda: A.launch_scaled_dot_product(x[0], x[1], out, B, Sq, D), {"layout": "[B*S][D]"}
+        if kind == "softmax":
+            return lambda: A.launch_softmax(sc, out, B, Sq), {"layout": "[B*S][S]"}
+        p = torch.softmax(sc, dim=-1).contiguous()
+        return lambda: A.launch_attention_weighted_sum(p, x[2], o, B, Sq, D), {"layout": "[B*S][S] x [B*S][D]"}
     E = H * D
     if dtype == "f32" and Sq == Sk:
         # the reference's planar [Q|K|V] buffer
@@ -181,6 +203,7 @@ def main():
         t_mfma = flops / peak
         t_hbm = nbytes / PEAK_HBM
         bound = "hbm" if t_hbm > t_mfma else "mfma"
+        # the null stream the helpers launch on is torch's default stream here
         tflops = flops / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = (t_hbm if bound == "hbm" else t_mfma) / (ms * 1e-3)

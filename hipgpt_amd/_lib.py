@@ -32,6 +32,9 @@ _f = ctypes.c_float
 SIGNATURES = {
     "hipgpt_attn_strerror": (ctypes.c_char_p, [_int]),
     "hipgpt_launch_multihead_attention": (None, [_vp, _vp, _vp, _int, _int, _int, _int]),
+    "hipgpt_launch_scaled_dot_product": (None, [_vp, _vp, _vp, _int, _int, _int]),
+    "hipgpt_launch_softmax": (None, [_vp, _vp, _int, _int]),
+    "hipgpt_launch_attention_weighted_sum": (None, [_vp, _vp, _vp, _int, _int, _int]),
     "hipgpt_attn_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_fwd": (
         _int,
@@ -48,8 +51,13 @@ SIGNATURES = {
         + [_f, _int, _vp, ctypes.c_size_t, _vp],
     ),
 }
-# The drop-in C++ symbol (HipGPT include/hip_kernels.h:39-43).
+# The drop-in C++ symbols (HipGPT include/hip_kernels.h:39-46).
 CXX_LAUNCH_SYMBOL = "_Z26launch_multihead_attentionPKfPfS1_iiii"
+CXX_HELPER_SYMBOLS = {
+    "launch_scaled_dot_product": "_Z25launch_scaled_dot_productPKfS0_Pfiii",
+    "launch_softmax": "_Z14launch_softmaxPKfPfii",
+    "launch_attention_weighted_sum": "_Z29launch_attention_weighted_sumPKfS0_Pfiii",
+}
 
 _lib = None
 _lock = threading.Lock()

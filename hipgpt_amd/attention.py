@@ -64,6 +64,38 @@ def launch_multihead_attention(d_qkv, d_output, d_attn_probs, B, S, E, H):
     )
 
 
+def _need_numel(name, t, n):
+    _need_cuda(name, t, torch.float32)
+    if t.numel() < n or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor with >= {n} elements")
+
+
+def launch_scaled_dot_product(Q, K, scores, B, S, D):
+    """HipGPT ``launch_scaled_dot_product`` (src/hip_kernels.cpp:455-472):
+    scores[b*S+i, j] = Q[b*S+i] . K[b*S+j] / sqrt(D); null stream."""
+    _need_numel("Q", Q, B * S * D)
+    _need_numel("K", K, B * S * D)
+    _need_numel("scores", scores, B * S * S)
+    _lib.lib().hipgpt_launch_scaled_dot_product(_ptr(Q), _ptr(K), _ptr(scores), B, S, D)
+
+
+def launch_softmax(scores, softmax_out, B, S):
+    """HipGPT ``launch_softmax`` (src/hip_kernels.cpp:478-509): row softmax
+    of [B*S, S]; null stream."""
+    _need_numel("scores", scores, B * S * S)
+    _need_numel("softmax_out", softmax_out, B * S * S)
+    _lib.lib().hipgpt_launch_softmax(_ptr(scores), _ptr(softmax_out), B, S)
+
+
+def launch_attention_weighted_sum(softmax, V, output, B, S, D):
+    """HipGPT ``launch_attention_weighted_sum`` (src/hip_kernels.cpp:512-532):
+    output[b*S+i] = sum_j softmax[b*S+i, j] V[b*S+j]; null stream."""
+    _need_numel("softmax", softmax, B * S * S)
+    _need_numel("V", V, B * S * D)
+    _need_numel("output", output, B * S * D)
+    _lib.lib().hipgpt_launch_attention_weighted_sum(_ptr(softmax), _ptr(V), _ptr(output), B, S, D)
+
+
 def qkv_planar(d_qkv, d_output, d_attn_probs, B, S, E, H, causal=False, stream=None):
     """Planar-layout forward with causal masking and an explicit stream."""
     _need_cuda("d_qkv", d_qkv, torch.float32)

@@ -93,6 +93,28 @@ void launch_multihead_attention(const float* d_qkv, float* d_output, float* d_at
                 S, E, H);
 }
 
+// Unfused helpers (src/hip_kernels.cpp:454-532): the reference launches them
+// unchecked on the null stream; so do these (a failed launch is reported on
+// stderr, as for the attention launcher).
+static void report(hipError_t e, const char* what) {
+    if (e != hipSuccess) fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+}
+
+void launch_scaled_dot_product(const float* Q, const float* K, float* scores, int B, int S, int D) {
+    if (B <= 0 || S <= 0 || D <= 0 || B > 65535) return;
+    report(hipgpt::launch_sdp(Q, K, scores, B, S, D, 0), "launch_scaled_dot_product");
+}
+
+void launch_softmax(const float* scores, float* softmax_out, int B, int S) {
+    if (B <= 0 || S <= 0) return;
+    report(hipgpt::launch_softmax_rows(scores, softmax_out, B, S, 0), "launch_softmax");
+}
+
+void launch_attention_weighted_sum(const float* softmax, const float* V, float* output, int B, int S, int D) {
+    if (B <= 0 || S <= 0 || D <= 0 || B > 65535) return;
+    report(hipgpt::launch_wsum(softmax, V, output, B, S, D, 0), "launch_attention_weighted_sum");
+}
+
 // ------------------------------------------------------------------- C ABI
 
 extern "C" {
@@ -111,6 +133,18 @@ const char* hipgpt_attn_strerror(int status) {
 void hipgpt_launch_multihead_attention(const float* d_qkv, float* d_output, float* d_attn_probs, int B,
                                        int S, int E, int H) {
     launch_multihead_attention(d_qkv, d_output, d_attn_probs, B, S, E, H);
+}
+
+void hipgpt_launch_scaled_dot_product(const float* Q, const float* K, float* scores, int B, int S, int D) {
+    launch_scaled_dot_product(Q, K, scores, B, S, D);
+}
+
+void hipgpt_launch_softmax(const float* scores, float* softmax_out, int B, int S) {
+    launch_softmax(scores, softmax_out, B, S);
+}
+
+void hipgpt_launch_attention_weighted_sum(const float* softmax, const float* V, float* output, int B, int S, int D) {
+    launch_attention_weighted_sum(softmax, V, output, B, S, D);
 }
 
 int hipgpt_attn_qkv_planar(const float* d_qkv, float* d_output, float* d_attn_probs, int B, int S, int E,

@@ -27,4 +27,9 @@ bool decode_supported(int D, int dtype);
 int decode_default_splits(int B, int H, int kv_len);
 hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream);
 
+// Unfused single-head helpers (HipGPT src/hip_kernels.cpp:454-532).
+hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int S, int D, hipStream_t s);
+hipError_t launch_softmax_rows(const float* in, float* out, int B, int S, hipStream_t s);
+hipError_t launch_wsum(const float* P, const float* V, float* O, int B, int S, int D, hipStream_t s);
+
 }  // namespace hipgpt

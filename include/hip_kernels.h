@@ -5,8 +5,8 @@
 // (C++ linkage; exported as _Z26launch_multihead_attentionPKfPfS1_iiii), so
 // TransformerLayer::self_attention_forward (src/transformer_layer.cpp:218-219)
 // links against libhipgpt_attn.so unchanged.  HipGPT's other declarations in
-// that header (GEMM, layer norm, loss, optimisers, the attention backward and
-// the unused unfused helpers) are not provided by this library.
+// that header (GEMM, layer norm, loss, optimisers, the attention backward)
+// are not provided by this library.
 
 #include <hip/hip_runtime.h>
 
@@ -25,3 +25,14 @@ void launch_multihead_attention(
     float* d_output,
     float* d_attn_probs,
     int B, int S, int E, int H);
+
+// HipGPT's unfused single-head helpers (include/hip_kernels.h:44-46,
+// src/hip_kernels.cpp:454-532).  Q, K, V, output are [B*S][D]; scores and
+// softmax are [B*S][S]; non-causal; fp32; asynchronous on the null stream;
+// allocate nothing.  Non-positive sizes launch nothing.
+//   scores = (Q K^T) * rsqrt(D)            per batch b
+//   softmax_out = row softmax of scores    (max-subtracted, sum clamped >= 1e-20)
+//   output = softmax V                     per batch b
+void launch_scaled_dot_product(const float* Q, const float* K, float* scores, int B, int S, int D);
+void launch_softmax(const float* scores, float* softmax_out, int B, int S);
+void launch_attention_weighted_sum(const float* softmax, const float* V, float* output, int B, int S, int D);

@@ -34,6 +34,15 @@ void hipgpt_launch_multihead_attention(const float* d_qkv, float* d_output,
                                        float* d_attn_probs, int B, int S,
                                        int E, int H);
 
+/* C-linkage twins of HipGPT's unfused helpers (include/hip_kernels.h:44-46),
+ * same contract as the C++ symbols declared in include/hip_kernels.h. */
+void hipgpt_launch_scaled_dot_product(const float* Q, const float* K,
+                                      float* scores, int B, int S, int D);
+void hipgpt_launch_softmax(const float* scores, float* softmax_out, int B,
+                           int S);
+void hipgpt_launch_attention_weighted_sum(const float* softmax, const float* V,
+                                          float* output, int B, int S, int D);
+
 /* HipGPT's planar [3][B*S][E] layout with the options the legacy symbol
  * lacks: causal masking (keys j <= i; probs written 0 above the diagonal so
  * HipGPT's backward, src/hip_kernels.cpp:1162-1243, stays exact) and a

@@ -357,3 +357,92 @@ int oracle_launch_multihead_attention(const float *qkv, float *out,
     p.variant = ((D == 64 || D == 32) && S <= 512) ? ORACLE_FLASH : ORACLE_FALLBACK; /* :422 */
     return oracle_attention(&p, nthreads);
 }
+
+/* ------------------------------------------------- unfused helpers
+ * Restated from src/hip_kernels.cpp:454-532 (one thread per token there,
+ * one row per loop iteration here; same per-element arithmetic). */
+
+typedef struct {
+    const float *a, *b;
+    float *out;
+    int B, S, D, kind, tid, nthreads;
+} helper_arg;
+
+static void *helper_worker(void *argp)
+{
+    const helper_arg *h = (const helper_arg *)argp;
+    const int S = h->S, D = h->D;
+    const int64_t rows = (int64_t)h->B * S;
+    for (int64_t t = h->tid; t < rows; t += h->nthreads) {
+        const int64_t base = (t / S) * (int64_t)S * D; /* (token / S) * S * D */
+        if (h->kind == 0) {                             /* scaled dot product */
+            const float inv = 1.0f / sqrtf((float)D);
+            for (int j = 0; j < S; ++j) {
+                float sum = 0.0f;
+                for (int d = 0; d < D; ++d)
+                    sum = fmaf(h->a[t * D + d], h->b[base + (int64_t)j * D + d], sum);
+                h->out[t * S + j] = sum * inv;
+            }
+        } else if (h->kind == 1) {                      /* softmax row */
+            const float *row = h->a + t * S;
+            float *o = h->out + t * S;
+            float mx = -1e30f;
+            for (int j = 0; j < S; ++j) mx = fmaxf(mx, row[j]);
+            float sum = 0.0f;
+            for (int j = 0; j < S; ++j) {
+                o[j] = expf(row[j] - mx);
+                sum += o[j];
+            }
+            const float inv = 1.0f / fmaxf(sum, 1e-20f);
+            for (int j = 0; j < S; ++j) o[j] *= inv;
+        } else {                                        /* weighted sum */
+            for (int d = 0; d < D; ++d) {
+                float sum = 0.0f;
+                for (int j = 0; j < S; ++j)
+                    sum = fmaf(h->a[t * S + j], h->b[base + (int64_t)j * D + d], sum);
+                h->out[t * D + d] = sum;
+            }
+        }
+    }
+    return NULL;
+}
+
+static void helper_run(const float *a, const float *b, float *out, int B, int S,
+                       int D, int kind, int nthreads)
+{
+    if (B <= 0 || S <= 0 || (kind != 1 && D <= 0)) return;
+    if (nthreads <= 0) nthreads = 1;
+    if (nthreads > 64) nthreads = 64;
+    pthread_t th[64];
+    helper_arg args[64];
+    for (int t = 0; t < nthreads; ++t)
+        args[t] = (helper_arg){a, b, out, B, S, D, kind, t, nthreads};
+    int started[64] = {0};
+    for (int t = 1; t < nthreads; ++t)
+        started[t] = pthread_create(&th[t], NULL, helper_worker, &args[t]) == 0;
+    helper_worker(&args[0]);
+    for (int t = 1; t < nthreads; ++t) {
+        if (started[t])
+            pthread_join(th[t], NULL);
+        else
+            helper_worker(&args[t]);
+    }
+}
+
+void oracle_scaled_dot_product(const float *Q, const float *K, float *scores,
+                               int B, int S, int D, int nthreads)
+{
+    helper_run(Q, K, scores, B, S, D, 0, nthreads);
+}
+
+void oracle_softmax_rows(const float *scores, float *out, int B, int S,
+                         int nthreads)
+{
+    helper_run(scores, NULL, out, B, S, 0, 1, nthreads);
+}
+
+void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
+                                   int B, int S, int D, int nthreads)
+{
+    helper_run(P, V, out, B, S, D, 2, nthreads);
+}

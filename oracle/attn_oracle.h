@@ -89,6 +89,19 @@ int oracle_launch_multihead_attention(const float *qkv, float *out,
                                       float *probs, int B, int S, int E, int H,
                                       int causal, int nthreads);
 
+/* Restatements of the reference's unfused single-head helpers
+ * (src/hip_kernels.cpp:454-532; declared include/hip_kernels.h:44-46).
+ * Q, K, V, O are [B*S][D]; scores / probs are [B*S][S]; non-causal. */
+/* scaled_dot_product_kernel :455-466: s = (sum_d q*k) * rsqrt(D) */
+void oracle_scaled_dot_product(const float *Q, const float *K, float *scores,
+                               int B, int S, int D, int nthreads);
+/* softmax_kernel :478-502: max from -1e30, expf, sum, * 1/max(sum, 1e-20) */
+void oracle_softmax_rows(const float *scores, float *out, int B, int S,
+                         int nthreads);
+/* attention_weighted_sum_kernel :513-525: o[d] = sum_j p_j * v_j[d] */
+void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
+                                   int B, int S, int D, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

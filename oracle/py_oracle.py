@@ -20,7 +20,8 @@ FALLBACK = 1
 __all__ = [
     "ORACLE_SO", "REF_SO", "FLASH", "FALLBACK", "splitmix64", "fill_normal",
     "round_bf16", "attention", "launch_multihead_attention", "ref_available",
-    "ref_lib", "planar_qkv", "seeded_planar", "seeded_bshd",
+    "ref_lib", "planar_qkv", "seeded_planar", "seeded_bshd", "scaled_dot_product",
+    "softmax_rows", "attention_weighted_sum",
 ]
 
 
@@ -59,6 +60,11 @@ def _oracle():
         L.oracle_attention_pairs.restype = ctypes.c_int
         L.oracle_attention_pairs.argtypes = [ctypes.POINTER(_Problem), ctypes.c_void_p,
                                              ctypes.c_int, ctypes.c_int]
+        for fn in ("oracle_scaled_dot_product", "oracle_attention_weighted_sum"):
+            getattr(L, fn).restype = None
+            getattr(L, fn).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
+        L.oracle_softmax_rows.restype = None
+        L.oracle_softmax_rows.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3
         L.oracle_launch_multihead_attention.restype = ctypes.c_int
         L.oracle_launch_multihead_attention.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -149,6 +155,34 @@ def launch_multihead_attention(qkv, B, S, E, H, causal=False, want_probs=True, n
     return out, probs
 
 
+def _nt(nthreads):
+    return nthreads if nthreads is not None else min(8, os.cpu_count() or 1)
+
+
+def scaled_dot_product(Q, K, B, S, D, nthreads=None):
+    """src/hip_kernels.cpp:455-466 on [B*S, D] inputs -> scores [B*S, S]."""
+    Q = np.ascontiguousarray(Q, dtype=np.float32); K = np.ascontiguousarray(K, dtype=np.float32)
+    out = np.zeros((B * S, S), dtype=np.float32)
+    _oracle().oracle_scaled_dot_product(Q.ctypes.data, K.ctypes.data, out.ctypes.data, B, S, D, _nt(nthreads))
+    return out
+
+
+def softmax_rows(scores, B, S, nthreads=None):
+    """src/hip_kernels.cpp:478-502: row softmax of [B*S, S] scores."""
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    out = np.zeros((B * S, S), dtype=np.float32)
+    _oracle().oracle_softmax_rows(scores.ctypes.data, out.ctypes.data, B, S, _nt(nthreads))
+    return out
+
+
+def attention_weighted_sum(P, V, B, S, D, nthreads=None):
+    """src/hip_kernels.cpp:513-525: [B*S, S] probs times [B*S, D] values."""
+    P = np.ascontiguousarray(P, dtype=np.float32); V = np.ascontiguousarray(V, dtype=np.float32)
+    out = np.zeros((B * S, D), dtype=np.float32)
+    _oracle().oracle_attention_weighted_sum(P.ctypes.data, V.ctypes.data, out.ctypes.data, B, S, D, _nt(nthreads))
+    return out
+
+
 def planar_qkv(qkv, B, S, E, H):
     """[B, S, H, D] views of the Q, K, V planes of a planar buffer."""
     D = E // H
@@ -191,5 +225,12 @@ def ref_lib():
         fn.restype = None
         fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
         L.launch = fn
+        for attr, sym, nargs in (("sdp", "_Z25launch_scaled_dot_productPKfS0_Pfiii", (3, 3)),
+                                 ("softmax", "_Z14launch_softmaxPKfPfii", (2, 2)),
+                                 ("wsum", "_Z29launch_attention_weighted_sumPKfS0_Pfiii", (3, 3))):
+            f = getattr(L, sym)
+            f.restype = None
+            f.argtypes = [ctypes.c_void_p] * nargs[0] + [ctypes.c_int] * nargs[1]
+            setattr(L, attr, f)
         _ref = L
     return _ref

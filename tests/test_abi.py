@@ -26,7 +26,8 @@ def declared_functions(path):
 def test_headers_declare_expected_entry_points():
     c_api = declared_functions(HEADERS[1])
     assert set(_lib.SIGNATURES) == c_api
-    assert declared_functions(HEADERS[0]) == {"launch_multihead_attention"}
+    assert declared_functions(HEADERS[0]) == {"launch_multihead_attention", "launch_scaled_dot_product",
+                                               "launch_softmax", "launch_attention_weighted_sum"}
 
 
 def test_library_exports_every_declared_symbol():
@@ -37,6 +38,8 @@ def test_library_exports_every_declared_symbol():
     assert hasattr(L, "_Z26launch_multihead_attentionPKfPfS1_iiii")
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True)
     assert " T _Z26launch_multihead_attentionPKfPfS1_iiii" in out.stdout
+    for sym in _lib.CXX_HELPER_SYMBOLS.values():  # include/hip_kernels.h:44-46, exact C++ names
+        assert f" T {sym}" in out.stdout, sym
 
 
 def test_strerror_and_host_validation():

@@ -265,3 +265,37 @@ def test_bf16_baseline_config_c3(dev, causal):
     want, _ = O.attention(rq, rk, rv, causal=causal, pairs=pairs, nthreads=3)
     for b, h in pairs:
         assert np.abs(got[b, :, h] - want[b, :, h]).max() <= TOL_BF16, (b, h)
+
+
+# ---------------------------------------------------------------- unfused helpers
+@pytest.mark.parametrize("B,S,D", [(1, 1, 8), (2, 33, 32), (1, 70, 48), (3, 64, 64), (2, 45, 128),
+                                   (1, 20, 160), (32, 256, 32)])
+def test_unfused_helpers_match_oracle_and_reference(dev, B, S, D):
+    """launch_scaled_dot_product / launch_softmax / launch_attention_weighted_sum
+    (include/hip_kernels.h:44-46) against the oracle and, where the reference
+    build is present, the reference's own kernels on the same device buffers."""
+    x = O.fill_normal(B * 31 + S * 7 + D, 3 * B * S * D).reshape(3, B * S, D)
+    dq, dk, dv = (dev_t(a) for a in x)
+    scores = torch.full((B * S, S), float("nan"), device=dev)
+    probs = torch.full((B * S, S), float("nan"), device=dev)
+    out = torch.full((B * S, D), float("nan"), device=dev)
+    A.launch_scaled_dot_product(dq, dk, scores, B, S, D)
+    A.launch_softmax(scores, probs, B, S)
+    A.launch_attention_weighted_sum(probs, dv, out, B, S, D)
+    ws = O.scaled_dot_product(x[0], x[1], B, S, D)
+    assert np.abs(host(scores) - ws).max() <= 1e-4
+    wp = O.softmax_rows(host(scores), B, S)  # same input as the GPU softmax saw
+    assert np.abs(host(probs) - wp).max() <= TOL_P
+    wo = O.attention_weighted_sum(host(probs), x[2], B, S, D)
+    assert np.abs(host(out) - wo).max() <= TOL_O
+    if O.ref_available():
+        ref = O.ref_lib()
+        rs = torch.zeros_like(scores)
+        rp = torch.zeros_like(probs)
+        ro = torch.zeros_like(out)
+        ref.sdp(dq.data_ptr(), dk.data_ptr(), rs.data_ptr(), B, S, D)
+        ref.softmax(scores.data_ptr(), rp.data_ptr(), B, S)
+        ref.wsum(probs.data_ptr(), dv.data_ptr(), ro.data_ptr(), B, S, D)
+        assert np.abs(host(scores) - host(rs)).max() <= 1e-4
+        assert np.abs(host(probs) - host(rp)).max() <= TOL_P
+        assert np.abs(host(out) - host(ro)).max() <= TOL_O

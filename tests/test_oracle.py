@@ -164,3 +164,27 @@ def test_oracle_matches_reference_golden(path):
     assert np.abs(out - g["out"].reshape(out.shape)).max() < 2e-6
     rows = g["prob_rows"]
     assert np.abs(probs[:, :, rows, :] - g["probs"]).max() < 1e-6
+
+
+@pytest.mark.parametrize("B,S,D", [(1, 1, 8), (2, 33, 32), (1, 70, 48), (3, 17, 64)])
+def test_unfused_helpers_match_bruteforce(B, S, D):
+    """scaled_dot_product / softmax / weighted_sum restatements
+    (src/hip_kernels.cpp:454-532) against numpy in float64."""
+    x = O.fill_normal(B * 100 + S + D, 3 * B * S * D).reshape(3, B * S, D)
+    s = O.scaled_dot_product(x[0], x[1], B, S, D)
+    q, k, v = (a.reshape(B, S, D).astype(np.float64) for a in x)
+    ref = (np.einsum("bid,bjd->bij", q, k) / np.sqrt(D)).reshape(B * S, S)
+    assert np.abs(s - ref).max() < 2e-6
+    p = O.softmax_rows(s, B, S)
+    e = np.exp(ref - ref.max(-1, keepdims=True))
+    e /= e.sum(-1, keepdims=True)
+    assert np.abs(p - e).max() < 1e-6
+    assert np.abs(p.sum(-1) - 1).max() < 1e-5
+    o = O.attention_weighted_sum(p, x[2], B, S, D)
+    ro = np.einsum("bij,bjd->bid", e.reshape(B, S, S), v).reshape(B * S, D)
+    assert np.abs(o - ro).max() < 2e-6
+    # composition equals the fused restatement (H = 1, planar layout)
+    qkv = np.concatenate([x[0].ravel(), x[1].ravel(), x[2].ravel()])
+    fused, probs = O.launch_multihead_attention(qkv, B, S, D, 1)
+    assert np.abs(fused - o).max() < 2e-6
+    assert np.abs(probs.reshape(B * S, S) - p).max() < 1e-6
