@@ -40,6 +40,12 @@ CONFIGS = {
     "a8_scores": (256, 1, 256, 256, 32, False, "f32", False, "sdp"),
     "a8_softmax": (256, 1, 256, 256, 32, False, "f32", False, "softmax"),
     "a8_wsum": (256, 1, 256, 256, 32, False, "f32", False, "wsum"),
+    # Attention backward on the forward's probs (src/hip_kernels.cpp:1159-1272)
+    # at the c1 / c2 shapes: causal through the extended entry point, and the
+    # drop-in symbol on non-causal probs.
+    "c1_bwd": (32, 8, 256, 256, 32, True, "f32", True, "bwd"),
+    "c1_bwd_legacy": (32, 8, 256, 256, 32, False, "f32", True, "bwd"),
+    "c2_bwd": (32, 8, 256, 256, 64, True, "f32", True, "bwd"),
 }
 
 
@@ -53,6 +59,11 @@ def work(cfg):
         return 0.0, 8 * B * Sq * Sk
     if kind == "wsum":  # read P, V; write O
         return 2.0 * B * Sq * Sk * D, 4 * (B * Sq * Sk + 2 * B * Sq * D)
+    if kind == "bwd":
+        # dP, dV, dQ, dK: 8 D flops per visible pair; read the visible probs,
+        # Q, K, V, dO; write dQ, dK, dV
+        pairs = Sq * (Sq + 1) // 2 if causal else Sq * Sk
+        return 8.0 * B * H * D * pairs, 4 * B * H * (pairs + 7 * Sq * D)
     if kind == "decode":
         pairs = Sk
     elif causal:
@@ -93,6 +104,19 @@ def make_call(cfg, torch, A, dev):
         p = torch.softmax(sc, dim=-1).contiguous()
         return lambda: A.launch_attention_weighted_sum(p, x[2], o, B, Sq, D), {"layout": "[B*S][S] x [B*S][D]"}
     E = H * D
+    if kind == "bwd":
+        qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)
+        go = torch.randn(B * Sq * E, device=dev, generator=g)
+        out = torch.empty(B * Sq, E, device=dev)
+        p = torch.empty(B, H, Sq, Sk, device=dev)
+        A.qkv_planar(qkv, out, p, B, Sq, E, H, causal=causal)  # the probs the forward hands over
+        grad = torch.empty(3 * B * Sq * E, device=dev)
+        if not causal:
+            return (lambda: A.launch_multihead_attention_backward(go, qkv, p, grad, B, Sq, E, H),
+                    {"layout": "planar [3][B*S][E]", "entry": "launch_multihead_attention_backward"})
+        ws = torch.empty(B * H * Sq, device=dev)
+        return (lambda: A.attention_backward(go, qkv, p, grad, B, Sq, E, H, causal=True, workspace=ws),
+                {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_bwd_qkv_planar"})
     if dtype == "f32" and Sq == Sk:
         # the reference's planar [Q|K|V] buffer
         qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)

@@ -35,6 +35,10 @@ SIGNATURES = {
     "hipgpt_launch_scaled_dot_product": (None, [_vp, _vp, _vp, _int, _int, _int]),
     "hipgpt_launch_softmax": (None, [_vp, _vp, _int, _int]),
     "hipgpt_launch_attention_weighted_sum": (None, [_vp, _vp, _vp, _int, _int, _int]),
+    "hipgpt_launch_multihead_attention_backward": (None, [_vp, _vp, _vp, _vp, _int, _int, _int, _int]),
+    "hipgpt_attn_bwd_workspace_bytes": (ctypes.c_size_t, [_int, _int, _int]),
+    "hipgpt_attn_bwd_qkv_planar": (
+        _int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]),
     "hipgpt_attn_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_fwd": (
         _int,
@@ -57,6 +61,7 @@ CXX_HELPER_SYMBOLS = {
     "launch_scaled_dot_product": "_Z25launch_scaled_dot_productPKfS0_Pfiii",
     "launch_softmax": "_Z14launch_softmaxPKfPfii",
     "launch_attention_weighted_sum": "_Z29launch_attention_weighted_sumPKfS0_Pfiii",
+    "launch_multihead_attention_backward": "_Z35launch_multihead_attention_backwardPKfS0_S0_Pfiiii",
 }
 
 _lib = None

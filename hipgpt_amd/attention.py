@@ -96,6 +96,39 @@ def launch_attention_weighted_sum(softmax, V, output, B, S, D):
     _lib.lib().hipgpt_launch_attention_weighted_sum(_ptr(softmax), _ptr(V), _ptr(output), B, S, D)
 
 
+def launch_multihead_attention_backward(d_grad_attn_output, d_qkv, d_softmax, d_grad_qkv, B, S, E, H):
+    """HipGPT ``launch_multihead_attention_backward`` (src/hip_kernels.cpp:1245-1272):
+    planar [dQ|dK|dV] from dO, the forward's planar Q|K|V and its probs.
+    Null stream; the C++ symbol aborts on a bad head split (raised here)."""
+    if H <= 0 or E % H != 0:
+        raise ValueError(f"Bad MHA config: E={E} H={H}")
+    n = B * S * E
+    _need_numel("d_grad_attn_output", d_grad_attn_output, n)
+    _need_numel("d_qkv", d_qkv, 3 * n)
+    _need_numel("d_softmax", d_softmax, B * H * S * S)
+    _need_numel("d_grad_qkv", d_grad_qkv, 3 * n)
+    _lib.lib().hipgpt_launch_multihead_attention_backward(
+        _ptr(d_grad_attn_output), _ptr(d_qkv), _ptr(d_softmax), _ptr(d_grad_qkv), B, S, E, H)
+
+
+def attention_backward(grad_out, qkv, probs, grad_qkv, B, S, E, H, causal=False, workspace=None, stream=None):
+    """Backward with a caller workspace and stream; ``causal`` skips the
+    probs tiles a causal forward zeroed."""
+    n = B * S * E
+    _need_numel("grad_out", grad_out, n)
+    _need_numel("qkv", qkv, 3 * n)
+    _need_numel("probs", probs, B * H * S * S)
+    _need_numel("grad_qkv", grad_qkv, 3 * n)
+    need = int(_lib.lib().hipgpt_attn_bwd_workspace_bytes(B, S, H))
+    if workspace is None:
+        workspace = torch.empty(max(1, need // 4), device=qkv.device, dtype=torch.float32)
+    rc = _lib.lib().hipgpt_attn_bwd_qkv_planar(
+        _ptr(grad_out), _ptr(qkv), _ptr(probs), _ptr(grad_qkv), B, S, E, H, int(bool(causal)),
+        _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream))
+    _lib.check(rc, "hipgpt_attn_bwd_qkv_planar")
+    return grad_qkv
+
+
 def qkv_planar(d_qkv, d_output, d_attn_probs, B, S, E, H, causal=False, stream=None):
     """Planar-layout forward with causal masking and an explicit stream."""
     _need_cuda("d_qkv", d_qkv, torch.float32)

@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 
 #include "../../include/hip_kernels.h"
 #include "../../include/hipgpt_attn.h"
@@ -115,6 +116,71 @@ void launch_attention_weighted_sum(const float* softmax, const float* V, float* 
     report(hipgpt::launch_wsum(softmax, V, output, B, S, D, 0), "launch_attention_weighted_sum");
 }
 
+// Attention backward (src/hip_kernels.cpp:1245-1272).  The planar buffers of
+// the forward; the B*H*S row-dot workspace comes from the caller or, for the
+// drop-in symbol (whose signature has no workspace), from a buffer cached per
+// device and grown on demand.
+namespace {
+
+hipgpt::BwdArgs planar_bwd_args(const float* go, const float* qkv, const float* probs, float* gqkv, int B, int S,
+                                int E, int H, int causal) {
+    const int64_t plane = (int64_t)B * S * E;
+    hipgpt::BwdArgs a{};
+    a.q = qkv;
+    a.k = qkv + plane;
+    a.v = qkv + 2 * plane;
+    a.go = go;
+    a.probs = probs;
+    a.dq = gqkv;
+    a.dk = gqkv + plane;
+    a.dv = gqkv + 2 * plane;
+    a.bs = (int64_t)S * E;
+    a.ts = E;
+    a.hs = E / H;
+    a.B = B;
+    a.H = H;
+    a.S = S;
+    a.D = E / H;
+    a.causal = causal;
+    a.scale = 1.0f / std::sqrt((float)a.D);
+    return a;
+}
+
+float* cached_bwd_workspace(size_t bytes) {
+    static std::mutex mu;
+    static void* buf[64] = {};
+    static size_t cap[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cap[dev] < bytes) {
+        if (buf[dev] && hipFree(buf[dev]) != hipSuccess) return nullptr;
+        buf[dev] = nullptr;
+        cap[dev] = 0;
+        if (hipMalloc(&buf[dev], bytes) != hipSuccess) return nullptr;
+        cap[dev] = bytes;
+    }
+    return static_cast<float*>(buf[dev]);
+}
+
+}  // namespace
+
+void launch_multihead_attention_backward(const float* d_grad_attn_output, const float* d_qkv, const float* d_softmax,
+                                         float* d_grad_qkv, int B, int S, int E, int H) {
+    if (H <= 0 || (E % H) != 0) {  // the reference divides by H unchecked; abort as the forward does
+        fprintf(stderr, "Bad MHA config: E=%d H=%d\n", E, H);
+        abort();
+    }
+    if (B <= 0 || S <= 0 || E <= 0) return;
+    hipgpt::BwdArgs a = planar_bwd_args(d_grad_attn_output, d_qkv, d_softmax, d_grad_qkv, B, S, E, H, 0);
+    a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
+    if (!a.dvec) {
+        fprintf(stderr, "launch_multihead_attention_backward: workspace allocation failed\n");
+        return;
+    }
+    report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
+}
+
 // ------------------------------------------------------------------- C ABI
 
 extern "C" {
@@ -145,6 +211,29 @@ void hipgpt_launch_softmax(const float* scores, float* softmax_out, int B, int S
 
 void hipgpt_launch_attention_weighted_sum(const float* softmax, const float* V, float* output, int B, int S, int D) {
     launch_attention_weighted_sum(softmax, V, output, B, S, D);
+}
+
+void hipgpt_launch_multihead_attention_backward(const float* d_grad_attn_output, const float* d_qkv,
+                                                const float* d_softmax, float* d_grad_qkv, int B, int S, int E,
+                                                int H) {
+    launch_multihead_attention_backward(d_grad_attn_output, d_qkv, d_softmax, d_grad_qkv, B, S, E, H);
+}
+
+size_t hipgpt_attn_bwd_workspace_bytes(int B, int S, int H) {
+    if (B <= 0 || S <= 0 || H <= 0) return 0;
+    return (size_t)B * H * S * sizeof(float);
+}
+
+int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv, const float* probs, float* grad_qkv, int B,
+                               int S, int E, int H, int causal, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    if (!grad_out || !qkv || !probs || !grad_qkv || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0)
+        return HIPGPT_ERR_INVALID;
+    if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if (!workspace || workspace_bytes < hipgpt_attn_bwd_workspace_bytes(B, S, H)) return HIPGPT_ERR_WORKSPACE;
+    hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, probs, grad_qkv, B, S, E, H, causal ? 1 : 0);
+    a.dvec = static_cast<float*>(workspace);
+    return from_hip(hipgpt::launch_attn_bwd(a, stream));
 }
 
 int hipgpt_attn_qkv_planar(const float* d_qkv, float* d_output, float* d_attn_probs, int B, int S, int E,

@@ -27,6 +27,19 @@ bool decode_supported(int D, int dtype);
 int decode_default_splits(int B, int H, int kv_len);
 hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream);
 
+// Attention backward on the forward's probs (HipGPT src/hip_kernels.cpp:1159-1272).
+// All [B][S][H][D] tensors share one (batch, token, head) stride set; dvec is
+// a B*H*S float workspace (row dots dO_i . (P V)_i).
+struct BwdArgs {
+    const float *q, *k, *v, *go, *probs;
+    float *dq, *dk, *dv, *dvec;
+    int64_t bs, ts, hs;
+    int B, H, S, D;
+    int causal;
+    float scale;
+};
+hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s);
+
 // Unfused single-head helpers (HipGPT src/hip_kernels.cpp:454-532).
 hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int S, int D, hipStream_t s);
 hipError_t launch_softmax_rows(const float* in, float* out, int B, int S, hipStream_t s);

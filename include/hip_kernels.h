@@ -5,8 +5,8 @@
 // (C++ linkage; exported as _Z26launch_multihead_attentionPKfPfS1_iiii), so
 // TransformerLayer::self_attention_forward (src/transformer_layer.cpp:218-219)
 // links against libhipgpt_attn.so unchanged.  HipGPT's other declarations in
-// that header (GEMM, layer norm, loss, optimisers, the attention backward)
-// are not provided by this library.
+// that header (GEMM, layer norm, loss, optimisers, embeddings) are not
+// provided by this library.
 
 #include <hip/hip_runtime.h>
 
@@ -36,3 +36,18 @@ void launch_multihead_attention(
 void launch_scaled_dot_product(const float* Q, const float* K, float* scores, int B, int S, int D);
 void launch_softmax(const float* scores, float* softmax_out, int B, int S);
 void launch_attention_weighted_sum(const float* softmax, const float* V, float* output, int B, int S, int D);
+
+// Attention backward on the forward's probabilities (include/hip_kernels.h:59-62,
+// src/hip_kernels.cpp:1159-1272; called from TransformerLayer::backward,
+// src/transformer_layer.cpp:285-286).
+//   d_grad_attn_output dO [B*S][E]; d_qkv the forward's planar [Q|K|V];
+//   d_softmax the forward's probs [B][H][S][S]; d_grad_qkv receives the planar
+//   [dQ|dK|dV], every element written (the reference memsets, then adds).
+// Non-causal as the reference; a causal forward's zero upper triangle gives the
+// causal gradient.  Asynchronous on the null stream.  Uses a B*H*S float
+// workspace cached per device (allocated on first use and when it must grow).
+// Aborts with "Bad MHA config" when H <= 0 or E % H != 0.
+void launch_multihead_attention_backward(
+    const float* d_grad_attn_output, const float* d_qkv, const float* d_softmax,
+    float* d_grad_qkv, int B, int S, int E, int H
+);

@@ -43,6 +43,25 @@ void hipgpt_launch_softmax(const float* scores, float* softmax_out, int B,
 void hipgpt_launch_attention_weighted_sum(const float* softmax, const float* V,
                                           float* output, int B, int S, int D);
 
+/* C-linkage twin of launch_multihead_attention_backward
+ * (include/hip_kernels.h; replaces src/hip_kernels.cpp:1159-1272). */
+void hipgpt_launch_multihead_attention_backward(const float* d_grad_attn_output,
+                                                const float* d_qkv,
+                                                const float* d_softmax,
+                                                float* d_grad_qkv, int B, int S,
+                                                int E, int H);
+
+/* Backward with a caller-owned workspace (hipgpt_attn_bwd_workspace_bytes:
+ * B*H*S floats), a stream, and a causal flag that skips tiles of the probs
+ * wholly above the diagonal (a causal forward wrote zeros there).  Same
+ * buffers as the drop-in; returns a status. */
+size_t hipgpt_attn_bwd_workspace_bytes(int B, int S, int H);
+int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv,
+                               const float* probs, float* grad_qkv, int B,
+                               int S, int E, int H, int causal,
+                               void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
 /* HipGPT's planar [3][B*S][E] layout with the options the legacy symbol
  * lacks: causal masking (keys j <= i; probs written 0 above the diagonal so
  * HipGPT's backward, src/hip_kernels.cpp:1162-1243, stays exact) and a

@@ -446,3 +446,46 @@ void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
 {
     helper_run(P, V, out, B, S, D, 2, nthreads);
 }
+
+/* ---------------------------------------------------- attention backward */
+int oracle_mha_backward(const float *grad_out, const float *qkv,
+                        const float *probs, float *grad_qkv, int B, int S,
+                        int E, int H)
+{
+    if (B <= 0 || S <= 0 || H <= 0 || E % H != 0) return -1;
+    const int D = E / H;
+    const int64_t plane = (int64_t)B * S * E;
+    const float *Q = qkv, *K = qkv + plane, *V = qkv + 2 * plane;
+    float *dQ = grad_qkv, *dK = grad_qkv + plane, *dV = grad_qkv + 2 * plane;
+    memset(grad_qkv, 0, (size_t)(3 * plane) * sizeof(float));
+    const float inv = 1.0f / sqrtf((float)D);
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h)
+            for (int i = 0; i < S; ++i) {
+                const int64_t ti = (int64_t)b * S + i;
+                const float *gho = grad_out + ti * E + h * D;
+                const float *q = Q + ti * E + h * D;
+                float *dq = dQ + ti * E + h * D;
+                const float *prow = probs + (((int64_t)b * H + h) * S + i) * S;
+                float ws = 0.0f;
+                for (int j = 0; j < S; ++j) {
+                    const float *v = V + ((int64_t)b * S + j) * E + h * D;
+                    ws = fmaf(prow[j], dot_fma(gho, v, D), ws);
+                }
+                for (int j = 0; j < S; ++j) {
+                    const int64_t tj = (int64_t)b * S + j;
+                    const float *k = K + tj * E + h * D;
+                    const float *v = V + tj * E + h * D;
+                    const float pij = prow[j];
+                    const float g = pij * (dot_fma(gho, v, D) - ws);
+                    float *dv = dV + tj * E + h * D;
+                    float *dk = dK + tj * E + h * D;
+                    for (int d = 0; d < D; ++d) {
+                        dv[d] += pij * gho[d];
+                        dq[d] = fmaf(g * k[d], inv, dq[d]);
+                        dk[d] += g * q[d] * inv;
+                    }
+                }
+            }
+    return 0;
+}

@@ -102,6 +102,19 @@ void oracle_softmax_rows(const float *scores, float *out, int B, int S,
 void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
                                    int B, int S, int D, int nthreads);
 
+/* Restatement of multihead_attention_backward_kernel + its launcher
+ * (src/hip_kernels.cpp:1159-1272) on the planar buffers: grad_qkv is
+ * [3][B*S][E] (dQ, dK, dV planes), fully overwritten (the launcher memsets
+ * it, :1260).  Per (b, h, query i), in the kernel's order:
+ *   pass 1 :1193-1200  ws = sum_j p_ij (gho . v_j)
+ *   pass 2 :1208-1242  g = p_ij (gho . v_j - ws); dV_j += p_ij gho;
+ *                      dQ_i += g k_j / sqrt(D); dK_j += g q_i / sqrt(D)
+ * Sums into dK/dV are made in (i, j) order here; the kernel's atomics add
+ * in an unspecified order (few-ulp differences, unpinned). */
+int oracle_mha_backward(const float *grad_out, const float *qkv,
+                        const float *probs, float *grad_qkv, int B, int S,
+                        int E, int H);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,7 @@ __all__ = [
     "ORACLE_SO", "REF_SO", "FLASH", "FALLBACK", "splitmix64", "fill_normal",
     "round_bf16", "attention", "launch_multihead_attention", "ref_available",
     "ref_lib", "planar_qkv", "seeded_planar", "seeded_bshd", "scaled_dot_product",
-    "softmax_rows", "attention_weighted_sum",
+    "softmax_rows", "attention_weighted_sum", "mha_backward",
 ]
 
 
@@ -65,6 +65,8 @@ def _oracle():
             getattr(L, fn).argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
         L.oracle_softmax_rows.restype = None
         L.oracle_softmax_rows.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3
+        L.oracle_mha_backward.restype = ctypes.c_int
+        L.oracle_mha_backward.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4
         L.oracle_launch_multihead_attention.restype = ctypes.c_int
         L.oracle_launch_multihead_attention.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -183,6 +185,18 @@ def attention_weighted_sum(P, V, B, S, D, nthreads=None):
     return out
 
 
+def mha_backward(grad_out, qkv, probs, B, S, E, H):
+    """Restatement of launch_multihead_attention_backward
+    (src/hip_kernels.cpp:1159-1272); returns grad_qkv [3*B*S*E]."""
+    g = np.ascontiguousarray(grad_out, dtype=np.float32)
+    x = np.ascontiguousarray(qkv, dtype=np.float32)
+    p = np.ascontiguousarray(probs, dtype=np.float32)
+    out = np.zeros(3 * B * S * E, dtype=np.float32)
+    if _oracle().oracle_mha_backward(g.ctypes.data, x.ctypes.data, p.ctypes.data, out.ctypes.data, B, S, E, H) != 0:
+        raise ValueError(f"Bad MHA config: E={E} H={H}")
+    return out
+
+
 def planar_qkv(qkv, B, S, E, H):
     """[B, S, H, D] views of the Q, K, V planes of a planar buffer."""
     D = E // H
@@ -225,6 +239,10 @@ def ref_lib():
         fn.restype = None
         fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
         L.launch = fn
+        f = getattr(L, "_Z35launch_multihead_attention_backwardPKfS0_S0_Pfiiii")
+        f.restype = None
+        f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4
+        L.backward = f
         for attr, sym, nargs in (("sdp", "_Z25launch_scaled_dot_productPKfS0_Pfiii", (3, 3)),
                                  ("softmax", "_Z14launch_softmaxPKfPfii", (2, 2)),
                                  ("wsum", "_Z29launch_attention_weighted_sumPKfS0_Pfiii", (3, 3))):

@@ -27,7 +27,8 @@ def test_headers_declare_expected_entry_points():
     c_api = declared_functions(HEADERS[1])
     assert set(_lib.SIGNATURES) == c_api
     assert declared_functions(HEADERS[0]) == {"launch_multihead_attention", "launch_scaled_dot_product",
-                                               "launch_softmax", "launch_attention_weighted_sum"}
+                                               "launch_softmax", "launch_attention_weighted_sum",
+                                               "launch_multihead_attention_backward"}
 
 
 def test_library_exports_every_declared_symbol():
@@ -61,15 +62,21 @@ def test_strerror_and_host_validation():
     assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 4) == 2 * 3 * 4 * 66 * 4
     assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 1) == 0
     assert L.hipgpt_attn_decode_default_splits(64, 12, 2048) >= 2
+    assert L.hipgpt_attn_bwd_workspace_bytes(2, 8, 3) == 2 * 3 * 8 * 4
+    assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 64, 2, 0, None, 0, None) == _lib.ERR_WORKSPACE
+    assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 63, 2, 0, p, 1 << 20, None) == _lib.ERR_INVALID
 
 
-@pytest.mark.parametrize("sym", ["hipgpt_launch_multihead_attention", "_Z26launch_multihead_attentionPKfPfS1_iiii"])
+@pytest.mark.parametrize("sym", ["hipgpt_launch_multihead_attention", "_Z26launch_multihead_attentionPKfPfS1_iiii",
+                                 "hipgpt_launch_multihead_attention_backward",
+                                 "_Z35launch_multihead_attention_backwardPKfS0_S0_Pfiiii"])
 @pytest.mark.parametrize("E,H", [(63, 2), (64, 0), (64, -1)])
 def test_bad_config_aborts_like_reference(sym, E, H):
+    nptr = 4 if "backward" in sym else 3
     code = (
         "import ctypes,sys; L=ctypes.CDLL(sys.argv[1]); f=getattr(L, sys.argv[2]);"
-        "f.argtypes=[ctypes.c_void_p]*3+[ctypes.c_int]*4;"
-        f"f(None,None,None,2,4,{E},{H})"
+        f"f.argtypes=[ctypes.c_void_p]*{nptr}+[ctypes.c_int]*4;"
+        f"f(*([None]*{nptr}),2,4,{E},{H})"
     )
     r = subprocess.run([sys.executable, "-c", code, _lib.LIB_PATH, sym], capture_output=True, text=True)
     assert r.returncode == -6, r  # SIGABRT

@@ -1,0 +1,152 @@
+"""GPU parity tests of the attention backward (HipGPT src/hip_kernels.cpp:1159-1272)
+through the C ABI: the drop-in launch_multihead_attention_backward and the
+extended hipgpt_attn_bwd_qkv_planar against the oracle restatement (itself
+pinned by finite differences), the reference's own kernel on the same device
+buffers where oracle/_ref is built, and float64 torch autograd.
+
+Bar: max-abs <= 1e-4 x max(1, max |gradient|) -- the fp32 sums over S keys or
+queries run in a different order than the reference's (which adds with
+atomics, so its own order varies from run to run).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from hipgpt_amd import attention as A
+from hipgpt_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def tol(want):
+    return 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
+def _inputs(B, S, E, H, causal=False, seed=0):
+    qkv = O.seeded_planar(seed + B * 7919 + S * 31 + E, B, S, E)
+    go = O.fill_normal(seed + 99 + S + E, B * S * E)
+    _, probs = O.launch_multihead_attention(qkv, B, S, E, H, causal=causal, want_probs=True)
+    return qkv, go, probs
+
+
+# D = 32/64/128 MFMA kernels, padded D (7, 16, 48, 96), generic D (160, 256),
+# S below / across / not a multiple of the 32-row tile.
+SHAPES = [
+    (1, 1, 32, 1), (2, 7, 64, 2), (1, 33, 128, 2), (2, 64, 256, 2), (1, 100, 96, 2),
+    (1, 45, 32, 2), (1, 70, 192, 2), (1, 40, 512, 2), (1, 9, 14, 2), (2, 300, 256, 4),
+    (1, 129, 128, 1), (1, 20, 320, 2),
+]
+
+
+@pytest.mark.parametrize("B,S,E,H", SHAPES)
+def test_drop_in_backward_matches_oracle(dev, B, S, E, H):
+    qkv, go, probs = _inputs(B, S, E, H)
+    want = O.mha_backward(go, qkv, probs, B, S, E, H)
+    d_g = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    A.launch_multihead_attention_backward(dev_t(go), dev_t(qkv), dev_t(probs), d_g, B, S, E, H)
+    got = host(d_g)
+    assert np.isfinite(got).all()  # every element written (no memset in the contract)
+    assert np.abs(got - want).max() <= tol(want)
+
+
+@pytest.mark.parametrize("B,S,E,H", [(2, 7, 64, 2), (1, 33, 128, 2), (2, 100, 256, 4), (1, 45, 96, 2),
+                                     (1, 40, 512, 2)])
+def test_drop_in_backward_matches_reference_kernel(dev, B, S, E, H):
+    if not O.ref_available():
+        pytest.skip("reference build oracle/_ref missing")
+    ref = O.ref_lib()
+    qkv, go, probs = _inputs(B, S, E, H, seed=5)
+    d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
+    ours = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    theirs = torch.full_like(ours, float("nan"))
+    A.launch_multihead_attention_backward(d_go, d_qkv, d_p, ours, B, S, E, H)
+    ref.backward(d_go.data_ptr(), d_qkv.data_ptr(), d_p.data_ptr(), theirs.data_ptr(), B, S, E, H)
+    t = host(theirs)
+    assert np.abs(host(ours) - t).max() <= tol(t)
+
+
+@pytest.mark.parametrize("B,S,E,H", [(2, 37, 64, 2), (1, 160, 128, 2), (2, 96, 256, 2), (1, 75, 96, 1),
+                                     (1, 50, 512, 2)])
+def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
+    """Causal probs: the extended entry point with causal=1 skips tiles above
+    the diagonal; the skipped terms are exact zeros, so the result equals the
+    unmasked drop-in bit for bit, and both match the oracle."""
+    qkv, go, probs = _inputs(B, S, E, H, causal=True, seed=3)
+    want = O.mha_backward(go, qkv, probs, B, S, E, H)
+    d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
+    g_c = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    g_n = torch.full_like(g_c, float("nan"))
+    ws = torch.empty(_lib.lib().hipgpt_attn_bwd_workspace_bytes(B, S, H) // 4, device=dev)
+    A.attention_backward(d_go, d_qkv, d_p, g_c, B, S, E, H, causal=True, workspace=ws)
+    A.launch_multihead_attention_backward(d_go, d_qkv, d_p, g_n, B, S, E, H)
+    got = host(g_c)
+    assert np.abs(got - want).max() <= tol(want)
+    if E // H <= 128:  # MFMA kernels: skipped tiles contribute exact zeros
+        assert np.array_equal(got, host(g_n))
+    else:
+        assert np.abs(got - host(g_n)).max() <= tol(want)
+
+
+def test_workspace_too_small_is_rejected(dev):
+    B, S, E, H = 1, 64, 128, 2
+    x = torch.zeros(3 * B * S * E, device=dev)
+    p = torch.zeros(B * H * S * S, device=dev)
+    small = torch.zeros(B * H * S - 1, device=dev)
+    with pytest.raises(_lib.HipgptError, match="workspace"):
+        A.attention_backward(x[: B * S * E], x, p, x.clone(), B, S, E, H, workspace=small)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_then_backward_matches_torch_autograd(dev, causal):
+    """HIP forward (probs) -> HIP backward against float64 torch autograd of the
+    planar attention on the CPU."""
+    B, S, E, H = 2, 80, 256, 4
+    D = E // H
+    qkv, go, _ = _inputs(B, S, E, H, seed=11)
+    d_qkv = dev_t(qkv)
+    out = torch.empty((B * S, E), device=dev)
+    probs = torch.empty((B, H, S, S), device=dev)
+    A.qkv_planar(d_qkv, out, probs, B, S, E, H, causal=causal)
+    grad = torch.empty(3 * B * S * E, device=dev)
+    ws = torch.empty(B * H * S, device=dev)
+    A.attention_backward(dev_t(go), d_qkv, probs, grad, B, S, E, H, causal=causal, workspace=ws)
+
+    x = torch.from_numpy(qkv.astype(np.float64)).requires_grad_(True)
+    q, k, v = (t.reshape(B, S, H, D).transpose(1, 2) for t in x.reshape(3, B * S, E))
+    s = q @ k.transpose(-1, -2).contiguous() / np.sqrt(D)
+    if causal:
+        s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    o = (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B * S, E)
+    o.backward(torch.from_numpy(go.astype(np.float64)).reshape(B * S, E))
+    want = x.grad.numpy()
+    assert np.abs(host(grad) - want).max() <= tol(want)
+
+
+CONFIGS = {  # the BASELINE forward configs whose probs buffer fits the oracle's time budget
+    "c1": (32, 256, 256, 8),
+    "c2": (32, 256, 512, 8),
+}
+
+
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_baseline_config_backward(dev, cfg):
+    """Backward at the BASELINE configs' full shapes, on the causal probs the
+    forward produces there, against the oracle on the whole tensor."""
+    B, S, E, H = CONFIGS[cfg]
+    qkv, go, probs = _inputs(B, S, E, H, causal=True, seed=21)
+    want = O.mha_backward(go, qkv, probs, B, S, E, H)
+    d_g = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    ws = torch.empty(B * H * S, device=dev)
+    A.attention_backward(dev_t(go), dev_t(qkv), dev_t(probs), d_g, B, S, E, H, causal=True, workspace=ws)
+    got = host(d_g)
+    assert np.abs(got - want).max() <= tol(want)

@@ -188,3 +188,36 @@ def test_unfused_helpers_match_bruteforce(B, S, D):
     fused, probs = O.launch_multihead_attention(qkv, B, S, D, 1)
     assert np.abs(fused - o).max() < 2e-6
     assert np.abs(probs.reshape(B * S, S) - p).max() < 1e-6
+
+
+def _np_planar_forward(qkv, B, S, E, H, causal):
+    q, k, v = (x.astype(np.float64) for x in O.planar_qkv(qkv, B, S, E, H))
+    o, p = np_attention(q, k, v, causal)
+    return o.reshape(B * S, E), p
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,S,E,H", [(1, 5, 8, 2), (2, 4, 6, 1), (1, 7, 12, 3)])
+def test_backward_restatement_matches_finite_differences(B, S, E, H, causal):
+    """oracle_mha_backward (src/hip_kernels.cpp:1159-1272) against central
+    differences of L = sum(dO * O(qkv)) computed in float64 brute force.  Every
+    planar element is perturbed, so a dropped Dq term, a missing scale, a swapped
+    dK/dV plane or a transposed probs index each fail.  With causal probs the
+    unmasked formula must give the causal gradient (P = 0 above the diagonal)."""
+    qkv = O.seeded_planar(B * 100 + S * 10 + E + int(causal), B, S, E)
+    go = O.fill_normal(7 + S, B * S * E).reshape(B * S, E)
+    _, p64 = _np_planar_forward(qkv, B, S, E, H, causal)
+    got = O.mha_backward(go, qkv, p64.astype(np.float32), B, S, E, H)
+    x = qkv.astype(np.float64)
+    num = np.zeros_like(x)
+    eps = 1e-5
+    for n in range(x.size):
+        xp = x.copy()
+        xp[n] += eps
+        lp = (go * _np_planar_forward(xp, B, S, E, H, causal)[0]).sum()
+        xp[n] -= 2 * eps
+        lm = (go * _np_planar_forward(xp, B, S, E, H, causal)[0]).sum()
+        num[n] = (lp - lm) / (2 * eps)
+    assert np.abs(got - num).max() < 2e-5 * max(1.0, np.abs(num).max())
+    with pytest.raises(ValueError, match="Bad MHA config"):
+        O.mha_backward(go, qkv, p64.astype(np.float32), B, S, E, 0)
