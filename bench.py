@@ -46,6 +46,13 @@ CONFIGS = {
     "c1_bwd": (32, 8, 256, 256, 32, True, "f32", True, "bwd"),
     "c1_bwd_legacy": (32, 8, 256, 256, 32, False, "f32", True, "bwd"),
     "c2_bwd": (32, 8, 256, 256, 64, True, "f32", True, "bwd"),
+    # The projections either side of the attention (launch_matmul_add_bias,
+    # src/transformer_layer.cpp:217, :220) as (M, N, K, -, -, ...): the c1
+    # layer (T = 8192 tokens, E = 256) and the GPT-2-small c3 layer (E = 768).
+    "gemm_qkv_c1": (8192, 768, 256, 0, 0, False, "f32", False, "gemm"),
+    "gemm_out_c1": (8192, 256, 256, 0, 0, False, "f32", False, "gemm"),
+    "gemm_qkv_c3": (8192, 2304, 768, 0, 0, False, "f32", False, "gemm"),
+    "gemm_out_c3": (8192, 768, 768, 0, 0, False, "f32", False, "gemm"),
 }
 
 
@@ -53,6 +60,9 @@ def work(cfg):
     """Algorithmic FLOPs (4*B*H*D*P, P visible pairs) and HBM bytes (Q, K, V
     read once, O written once, plus probs when written)."""
     B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+    if kind == "gemm":  # A [M, K] @ W [K, N] + bias: read A, W, bias; write C
+        M, N, K = B, H, Sq
+        return 2.0 * M * N * K, 4 * (M * K + K * N + N + M * N)
     if kind == "sdp":  # read Q, K; write scores
         return 2.0 * B * Sq * Sk * D, 4 * (2 * B * Sq * D + B * Sq * Sk)
     if kind == "softmax":  # read and write B*S*S (no flops counted)
@@ -92,6 +102,16 @@ def make_call(cfg, torch, A, dev):
         ns = A.decode_default_splits(B, H, Sk)
         ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
         return lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws), {"splits": ns}
+    if kind == "gemm":
+        from hipgpt_amd import projection as P
+
+        M, N, K = B, H, Sq
+        a = torch.randn(M, K, device=dev, generator=g)
+        w = torch.randn(K, N, device=dev, generator=g)
+        bias = torch.randn(N, device=dev, generator=g)
+        c = torch.empty(M, N, device=dev)
+        return (lambda: P.launch_matmul_add_bias(a, w, bias, c, M, K, N),
+                {"entry": "launch_matmul_add_bias", "M": M, "N": N, "K": K})
     if kind in ("sdp", "softmax", "wsum"):
         x = torch.randn(3, B * Sq, D, device=dev, generator=g)
         sc = torch.randn(B * Sq, Sk, device=dev, generator=g)

@@ -23,6 +23,9 @@ ERR_WORKSPACE = -4
 F32 = 0
 BF16 = 1
 
+QKV_ROWS = 0
+QKV_PLANAR = 1
+
 # Entry points declared in include/*.h, with their ctypes signatures.
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -46,6 +49,11 @@ SIGNATURES = {
         + [_i64] * 12
         + [_f, _int, _int, _vp],
     ),
+    "hipgpt_launch_matmul": (None, [_vp, _vp, _vp, _int, _int, _int]),
+    "hipgpt_launch_matmul_add_bias": (None, [_vp, _vp, _vp, _vp, _int, _int, _int]),
+    "hipgpt_gemm_bias": (
+        _int, [_vp, _vp, _vp, _vp, _int, _int, _int, _i64, _i64, _i64, _int, _i64, _int, _vp]),
+    "hipgpt_qkv_projection": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_decode_default_splits": (_int, [_int, _int, _int]),
     "hipgpt_attn_decode_workspace_bytes": (ctypes.c_size_t, [_int, _int, _int, _int]),
     "hipgpt_attn_decode": (
@@ -62,6 +70,8 @@ CXX_HELPER_SYMBOLS = {
     "launch_softmax": "_Z14launch_softmaxPKfPfii",
     "launch_attention_weighted_sum": "_Z29launch_attention_weighted_sumPKfS0_Pfiii",
     "launch_multihead_attention_backward": "_Z35launch_multihead_attention_backwardPKfS0_S0_Pfiiii",
+    "launch_matmul": "_Z13launch_matmulPKfS0_Pfiii",
+    "launch_matmul_add_bias": "_Z22launch_matmul_add_biasPKfS0_S0_Pfiii",
 }
 
 _lib = None

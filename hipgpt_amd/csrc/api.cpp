@@ -181,6 +181,40 @@ void launch_multihead_attention_backward(const float* d_grad_attn_output, const 
     report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
 }
 
+// GEMMs either side of the attention (src/hip_kernels.cpp:102-154): the
+// reference's naming, A [M][N] x B [N][K] -> C [M][K].
+namespace {
+
+hipgpt::GemmArgs ref_gemm_args(const float* A, const float* B, const float* bias, float* C, int M, int N, int K) {
+    hipgpt::GemmArgs g{};
+    g.A = A;
+    g.W = B;
+    g.bias = bias;
+    g.C = C;
+    g.M = M;
+    g.N = K;
+    g.K = N > 0 ? N : 0;
+    g.lda = N > 0 ? N : 0;
+    g.ldw = K;
+    g.ldc = K;
+    g.seg_w = K;
+    g.seg_stride = 0;
+    g.out_bf16 = 0;
+    return g;
+}
+
+}  // namespace
+
+void launch_matmul(const float* A, const float* B, float* C, int M, int N, int K) {
+    if (M <= 0 || K <= 0) return;  // the reference's grid would be empty
+    report(hipgpt::launch_gemm(ref_gemm_args(A, B, nullptr, C, M, N, K), 0), "launch_matmul");
+}
+
+void launch_matmul_add_bias(const float* A, const float* B, const float* bias, float* C, int M, int N, int K) {
+    if (M <= 0 || K <= 0) return;
+    report(hipgpt::launch_gemm(ref_gemm_args(A, B, bias, C, M, N, K), 0), "launch_matmul_add_bias");
+}
+
 // ------------------------------------------------------------------- C ABI
 
 extern "C" {
@@ -322,6 +356,47 @@ int hipgpt_attn_decode(const float* q, const float* k, const float* v, float* o,
     a.D = D;
     a.qscale = default_scale(D, scale) * hipgpt::kLog2e;
     return from_hip(hipgpt::launch_decode(a, hipgpt::kF32, ns, static_cast<float*>(workspace), stream));
+}
+
+void hipgpt_launch_matmul(const float* A, const float* B, float* C, int M, int N, int K) {
+    launch_matmul(A, B, C, M, N, K);
+}
+
+void hipgpt_launch_matmul_add_bias(const float* A, const float* B, const float* bias, float* C, int M, int N,
+                                   int K) {
+    launch_matmul_add_bias(A, B, bias, C, M, N, K);
+}
+
+int hipgpt_gemm_bias(const float* A, const float* W, const float* bias, void* C, int M, int N, int K, int64_t lda,
+                     int64_t ldw, int64_t ldc, int seg_w, int64_t seg_stride, int out_dtype, hipStream_t stream) {
+    if (!C || M <= 0 || N <= 0 || K < 0 || (K > 0 && (!A || !W))) return HIPGPT_ERR_INVALID;
+    if (lda < K || ldw < N || seg_w < 1 || seg_w > N || ldc < seg_w || seg_stride < 0) return HIPGPT_ERR_INVALID;
+    if (out_dtype != HIPGPT_F32 && out_dtype != HIPGPT_BF16) return HIPGPT_ERR_INVALID;
+    hipgpt::GemmArgs g{};
+    g.A = A;
+    g.W = W;
+    g.bias = bias;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.lda = lda;
+    g.ldw = ldw;
+    g.ldc = ldc;
+    g.seg_w = seg_w;
+    g.seg_stride = seg_stride;
+    g.out_bf16 = out_dtype == HIPGPT_BF16;
+    return from_hip(hipgpt::launch_gemm(g, stream));
+}
+
+int hipgpt_qkv_projection(const float* x, const float* w_qkv, const float* b_qkv, void* out, int T, int E, int layout,
+                          int out_dtype, hipStream_t stream) {
+    if (T <= 0 || E <= 0 || (int64_t)3 * E > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if (layout != HIPGPT_QKV_ROWS && layout != HIPGPT_QKV_PLANAR) return HIPGPT_ERR_INVALID;
+    const int N = 3 * E;
+    if (layout == HIPGPT_QKV_ROWS)
+        return hipgpt_gemm_bias(x, w_qkv, b_qkv, out, T, N, E, E, N, N, N, 0, out_dtype, stream);
+    return hipgpt_gemm_bias(x, w_qkv, b_qkv, out, T, N, E, E, N, E, E, (int64_t)T * E, out_dtype, stream);
 }
 
 }  // extern "C"

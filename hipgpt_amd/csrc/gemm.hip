@@ -1,0 +1,292 @@
+// gemm.hip -- fp32 GEMM + bias on gfx950 MFMA: the projections either side
+// of the attention (QKV projection and output projection).
+//
+// Replaces matmul_add_bias_tiled_kernel / launch_matmul_add_bias and
+// matmul_tiled_kernel / launch_matmul (HipGPT src/hip_kernels.cpp:113-154,
+// :70-109), called from TransformerLayer::self_attention_forward
+// (src/transformer_layer.cpp:217, :220):
+//     C[m][n] = sum_k A[m][k] W[k][n] (+ bias[n])
+// with A [M][K] (row stride lda), W [K][N] (row stride ldw).  Output column
+// n goes to C + (n / seg_w) * seg_stride + m * ldc + n % seg_w, which is the
+// plain row-major [M][N] buffer for seg_w = N and, for the QKV projection
+// (N = 3E, seg_w = E, seg_stride = M*E), the planar [Q|K|V] buffer the
+// attention launcher reads.  Output fp32 or bf16 (RNE).
+//
+// Tiling: a workgroup owns a BM x BN tile of C and walks K in steps of 32.
+// Each wave computes a WM x WN sub-tile as C^T = W^T A^T on
+// v_mfma_f32_32x32x2_f32, so an accumulator register group holds four
+// consecutive output columns of one row (16-byte stores, 16-byte bias loads).
+// Operand staging: global -> registers -> LDS, double buffered, one barrier
+// per k-tile; the next tile's global loads are in flight during the MFMAs.
+//   A tile [BM][32] (pitch 36 floats): lane (c, h) reads row c, k = 16h + s as
+//     ds_read_b128 (four k-steps per read).
+//   W tile [32][BN] (pitch BN+4, second half of the k rows shifted by 32
+//     floats so the two lane halves read different banks): lane (c, h) reads
+//     W[16h + s][c] as one dword per k-step.
+// MFMA 32x32x2 f32 operand layout (lane l, c = l & 31, h = l >> 5): A-operand
+// value = row c of the MFMA's M dim, B-operand value = column c of its N dim,
+// both at contraction index h of the step; here contraction index k = 16h + s
+// at step s, the same bijection for both operands.
+#include "common.h"
+#include "kernels.h"
+
+namespace hipgpt {
+
+namespace {
+
+constexpr int GBK = 32;         // k per tile
+constexpr int APITCH = GBK + 4; // A tile row pitch, floats
+
+template <int BM, int BN, int WM, int WN>
+struct Cfg {
+    static constexpr int WAVES_M = BM / WM;
+    static constexpr int WAVES_N = BN / WN;
+    static constexpr int NW = WAVES_M * WAVES_N;
+    static constexpr int NT = NW * 64;
+    static constexpr int MB = WM / 32;  // m blocks per wave (MFMA N dim)
+    static constexpr int NB = WN / 32;  // n blocks per wave (MFMA M dim)
+    static constexpr int WPITCH = BN + 4;
+    static constexpr int A_ELEMS = BM * APITCH;
+    static constexpr int W_ELEMS = GBK * WPITCH + 32;
+    static constexpr int STAGE = A_ELEMS + W_ELEMS;
+    static constexpr int A_CHUNKS = BM * GBK / 4;
+    static constexpr int W_CHUNKS = GBK * BN / 4;
+    static constexpr int A_PER = A_CHUNKS / NT;
+    static constexpr int W_PER = W_CHUNKS / NT;
+    static_assert(A_CHUNKS % NT == 0 && W_CHUNKS % NT == 0, "tile loads must split evenly over the workgroup");
+    static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % WM == 0 && BN % WN == 0, "bad tile shape");
+    // W row r of the tile lives at r * WPITCH + (r >= 16 ? 32 : 0).
+    __device__ __forceinline__ static int wrow(int r) { return r * WPITCH + ((r >> 4) << 5); }
+};
+
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+template <int BM, int BN, int WM, int WN, bool VEC, bool BF16OUT>
+__global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(GemmArgs g) {
+    using C = Cfg<BM, BN, WM, WN>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * C::STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int tiles_n = (g.N + BN - 1) / BN;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int wm0 = (wave / C::WAVES_N) * WM;  // wave's rows within the tile
+    const int wn0 = (wave % C::WAVES_N) * WN;  // wave's columns within the tile
+    const int K = g.K;
+    const int nkt = (K + GBK - 1) / GBK;
+
+    // ---- global -> register staging of one k-tile ----
+    floatx4 ar[C::A_PER], wr[C::W_PER];
+    __amdgpu_buffer_rsrc_t ars, wrs;
+    int aoff[C::A_PER], woff[C::W_PER];
+    if constexpr (VEC) {
+        const int rows = min(BM, g.M - m0);
+        const int cols = min(BN, g.N - n0);
+        ars = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.A + (int64_t)m0 * g.lda), 0,
+                                                (int)(((int64_t)(rows - 1) * g.lda + K) * 4), kBufferFlags);
+        wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.W + n0), 0,
+                                                (int)(((int64_t)(K - 1) * g.ldw + cols) * 4), kBufferFlags);
+#pragma unroll
+        for (int i = 0; i < C::A_PER; ++i) {
+            const int f = tid + i * C::NT;
+            aoff[i] = (int)(((f >> 3) * g.lda + (f & 7) * 4) * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < C::W_PER; ++i) {
+            const int f = tid + i * C::NT;
+            woff[i] = (int)(((f / (BN / 4)) * g.ldw + (f % (BN / 4)) * 4) * 4);
+        }
+    }
+    auto load = [&](int kt) {
+        const int k0 = kt * GBK;
+#pragma unroll
+        for (int i = 0; i < C::A_PER; ++i) {
+            const int f = tid + i * C::NT;
+            const int r = f >> 3, kc = (f & 7) * 4;
+            if constexpr (VEC) {
+                // rows past M read as zero (buffer range); k past K is masked
+                // here because it would read the next row's values
+                const floatx4 v = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[i] + k0 * 4, 0, 0));
+                ar[i] = (k0 + kc < K) ? v : zero4();
+            } else {
+                const int m = m0 + r;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = k0 + kc + j;
+                    ar[i][j] = (m < g.M && k < K) ? g.A[(int64_t)m * g.lda + k] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::W_PER; ++i) {
+            const int f = tid + i * C::NT;
+            const int kr = f / (BN / 4), nc = (f % (BN / 4)) * 4;
+            if constexpr (VEC) {
+                // rows past K read as zero; columns past N only feed outputs
+                // that are never stored
+                wr[i] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[i] + (int)((int64_t)k0 * g.ldw * 4), 0, 0));
+            } else {
+                const int k = k0 + kr;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = n0 + nc + j;
+                    wr[i][j] = (k < K && n < g.N) ? g.W[(int64_t)k * g.ldw + n] : 0.f;
+                }
+            }
+        }
+    };
+    auto store = [&](float* st) {
+#pragma unroll
+        for (int i = 0; i < C::A_PER; ++i) {
+            const int f = tid + i * C::NT;
+            *reinterpret_cast<floatx4*>(st + (f >> 3) * APITCH + (f & 7) * 4) = ar[i];
+        }
+        float* ws = st + C::A_ELEMS;
+#pragma unroll
+        for (int i = 0; i < C::W_PER; ++i) {
+            const int f = tid + i * C::NT;
+            *reinterpret_cast<floatx4*>(ws + C::wrow(f / (BN / 4)) + (f % (BN / 4)) * 4) = wr[i];
+        }
+    };
+
+    floatx16 acc[C::NB][C::MB];
+#pragma unroll
+    for (int i = 0; i < C::NB; ++i)
+#pragma unroll
+        for (int j = 0; j < C::MB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    auto compute = [&](const float* st) {
+        const float* As = st + (wm0 + c) * APITCH + h * 16;
+        const float* Ws = st + C::A_ELEMS + wn0 + c;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            floatx4 av[C::MB];
+#pragma unroll
+            for (int j = 0; j < C::MB; ++j) av[j] = *reinterpret_cast<const floatx4*>(As + j * 32 * APITCH + 4 * q);
+            float wv[C::NB][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int row = C::wrow(h * 16 + 4 * q + u);
+#pragma unroll
+                for (int i = 0; i < C::NB; ++i) wv[i][u] = Ws[row + 32 * i];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int i = 0; i < C::NB; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::MB; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[i][u], av[j][u], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    if (nkt > 0) {
+        load(0);
+        store(lds);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nkt; ++kt) {
+        if (kt + 1 < nkt) load(kt + 1);
+        compute(lds + (kt & 1) * C::STAGE);
+        if (kt + 1 < nkt) store(lds + ((kt + 1) & 1) * C::STAGE);
+        __syncthreads();
+    }
+
+    // ---- epilogue: + bias, store (register group q -> columns 8q + 4h .. +3) ----
+#pragma unroll
+    for (int i = 0; i < C::NB; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn0 + 32 * i + 8 * q + 4 * h;
+            floatx4 bv = zero4();
+            if (g.bias) {
+                if (VEC) {
+                    if (n < g.N) bv = *reinterpret_cast<const floatx4*>(g.bias + n);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) bv[u] = (n + u < g.N) ? g.bias[n + u] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < C::MB; ++j) {
+                const int m = m0 + wm0 + 32 * j + c;
+                if (m >= g.M) continue;
+                floatx4 v;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = acc[i][j][4 * q + u] + bv[u];
+                if (VEC) {
+                    if (n >= g.N) continue;
+                    const int64_t off = (int64_t)(n / g.seg_w) * g.seg_stride + (int64_t)m * g.ldc + n % g.seg_w;
+                    if (BF16OUT) {
+                        bf16x4 o;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) o[u] = (__bf16)v[u];
+                        *reinterpret_cast<bf16x4*>(static_cast<__bf16*>(g.C) + off) = o;
+                    } else {
+                        *reinterpret_cast<floatx4*>(static_cast<float*>(g.C) + off) = v;
+                    }
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int nn = n + u;
+                        if (nn >= g.N) break;
+                        const int64_t off = (int64_t)(nn / g.seg_w) * g.seg_stride + (int64_t)m * g.ldc + nn % g.seg_w;
+                        if (BF16OUT)
+                            static_cast<__bf16*>(g.C)[off] = (__bf16)v[u];
+                        else
+                            static_cast<float*>(g.C)[off] = v[u];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, bool VEC>
+hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
+    const int64_t tiles = (int64_t)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    if (tiles <= 0 || tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
+    constexpr int NT = Cfg<BM, BN, WM, WN>::NT;
+    if (g.out_bf16)
+        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, VEC, true>), dim3((unsigned)tiles), dim3(NT), 0, s, g);
+    else
+        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, VEC, false>), dim3((unsigned)tiles), dim3(NT), 0, s, g);
+    return hipGetLastError();
+}
+
+// Tile shape per problem: the 128 x 64 tile when it yields at least two
+// workgroups per CU, else 64 x 64 (more, smaller tiles fill the 256 CUs).
+#ifndef HIPGPT_GEMM_BIG_MIN_TILES
+#define HIPGPT_GEMM_BIG_MIN_TILES 512
+#endif
+
+template <bool VEC>
+hipError_t launch_vec(const GemmArgs& g, hipStream_t s) {
+    const int64_t big = (int64_t)((g.M + 127) / 128) * ((g.N + 63) / 64);
+    if (big >= HIPGPT_GEMM_BIG_MIN_TILES) return launch_cfg<128, 64, 64, 32, VEC>(g, s);
+    return launch_cfg<64, 64, 32, 32, VEC>(g, s);
+}
+
+}  // namespace
+
+bool gemm_vec_ok(const GemmArgs& g) {
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    // 32-bit buffer offsets: W rows up to K + 32, A rows up to 128 past a tile's first row
+    const int64_t wbytes = ((int64_t)(g.K + GBK) * g.ldw + 128) * 4;
+    const int64_t abytes = ((int64_t)128 * g.lda + g.K + 2 * GBK) * 4;
+    return al(g.A) && al(g.W) && al(g.C) && (!g.bias || al(g.bias)) && g.K % 4 == 0 && g.N % 4 == 0 &&
+           g.lda % 4 == 0 && g.ldw % 4 == 0 && g.ldc % 4 == 0 && g.seg_w % 4 == 0 && g.seg_stride % 4 == 0 &&
+           wbytes < ((int64_t)1 << 31) && abytes < ((int64_t)1 << 31);
+}
+
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
+    return gemm_vec_ok(g) ? launch_vec<true>(g, s) : launch_vec<false>(g, s);
+}
+
+}  // namespace hipgpt

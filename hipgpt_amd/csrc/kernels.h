@@ -45,4 +45,22 @@ hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int 
 hipError_t launch_softmax_rows(const float* in, float* out, int B, int S, hipStream_t s);
 hipError_t launch_wsum(const float* P, const float* V, float* O, int B, int S, int D, hipStream_t s);
 
+// fp32 GEMM + bias (HipGPT src/hip_kernels.cpp:70-154):
+//   C[m][n] = sum_k A[m][k] W[k][n] (+ bias[n]), output column n stored at
+//   C + (n / seg_w) * seg_stride + m * ldc + n % seg_w, fp32 or bf16.
+struct GemmArgs {
+    const float* A;
+    const float* W;
+    const float* bias;  // may be null
+    void* C;
+    int M, N, K;
+    int64_t lda, ldw, ldc;
+    int seg_w;
+    int64_t seg_stride;
+    int out_bf16;
+};
+// True when the 16-byte vector path applies (alignment, multiples of 4).
+bool gemm_vec_ok(const GemmArgs& g);
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t s);
+
 }  // namespace hipgpt

@@ -1,5 +1,6 @@
 #pragma once
-// hip_kernels.h -- drop-in declaration of HipGPT's attention forward launcher.
+// hip_kernels.h -- drop-in declarations of HipGPT's attention launchers and
+// of the GEMMs either side of the attention.
 //
 // The signature is the one HipGPT declares in include/hip_kernels.h:39-43
 // (C++ linkage; exported as _Z26launch_multihead_attentionPKfPfS1_iiii), so
@@ -51,3 +52,14 @@ void launch_multihead_attention_backward(
     const float* d_grad_attn_output, const float* d_qkv, const float* d_softmax,
     float* d_grad_qkv, int B, int S, int E, int H
 );
+
+// fp32 GEMMs of the projections either side of the attention
+// (include/hip_kernels.h:6-7; src/hip_kernels.cpp:70-154; called from
+// TransformerLayer::self_attention_forward, src/transformer_layer.cpp:217
+// (QKV, N = E, K = 3E) and :220 (output projection, N = K = E)).
+//   A [M][N], B [N][K], bias [K], C [M][K], all row-major fp32:
+//   C = A B (+ bias), on fp32 MFMA.  Asynchronous on the null stream;
+//   allocate nothing; M <= 0 or K <= 0 launches nothing; N <= 0 gives
+//   C = bias (zero for launch_matmul), as the reference's loop does.
+void launch_matmul(const float* A, const float* B, float* C, int M, int N, int K);
+void launch_matmul_add_bias(const float* A, const float* B, const float* bias, float* C, int M, int N, int K);

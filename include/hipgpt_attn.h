@@ -24,6 +24,9 @@ enum {
 
 enum { HIPGPT_F32 = 0, HIPGPT_BF16 = 1 };
 
+/* Output layouts of hipgpt_qkv_projection. */
+enum { HIPGPT_QKV_ROWS = 0, HIPGPT_QKV_PLANAR = 1 };
+
 /* Text for a status code. */
 const char* hipgpt_attn_strerror(int status);
 
@@ -104,6 +107,38 @@ int hipgpt_attn_decode(const float* q, const float* k, const float* v,
                        int64_t o_bs, int64_t o_hs,
                        float scale, int num_splits, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
+
+/* ---- projections either side of the attention (fp32 MFMA GEMM) ---- */
+
+/* C-linkage twins of launch_matmul / launch_matmul_add_bias
+ * (include/hip_kernels.h; replace src/hip_kernels.cpp:70-154). */
+void hipgpt_launch_matmul(const float* A, const float* B, float* C, int M,
+                          int N, int K);
+void hipgpt_launch_matmul_add_bias(const float* A, const float* B,
+                                   const float* bias, float* C, int M, int N,
+                                   int K);
+
+/* General GEMM + bias: C[m][n] = sum_k A[m][k] W[k][n] (+ bias[n]).
+ *   A [M][K] row stride lda; W [K][N] row stride ldw; bias [N] or NULL.
+ *   Output column n is stored at C + (n / seg_w) * seg_stride + m * ldc
+ *   + n % seg_w (elements of out_dtype): seg_w = N gives a row-major [M][N]
+ *   buffer; seg_w = N/3, seg_stride = M*N/3 splits a QKV projection into
+ *   planar [3][M][N/3].  out_dtype HIPGPT_F32 or HIPGPT_BF16 (RNE).
+ *   Requires M, N >= 1, K >= 0, lda >= K, ldw >= N, 1 <= seg_w <= N,
+ *   ldc >= seg_w, seg_stride >= 0. */
+int hipgpt_gemm_bias(const float* A, const float* W, const float* bias,
+                     void* C, int M, int N, int K, int64_t lda, int64_t ldw,
+                     int64_t ldc, int seg_w, int64_t seg_stride,
+                     int out_dtype, hipStream_t stream);
+
+/* HipGPT's QKV projection (src/transformer_layer.cpp:217): x [T][E] times
+ * w_qkv [E][3E] plus b_qkv [3E].  layout HIPGPT_QKV_ROWS writes the
+ * reference's [T][3E] buffer; HIPGPT_QKV_PLANAR writes [3][T][E], so that
+ * plane p row t is projection p of token t in the layout the attention
+ * launchers read.  out_dtype HIPGPT_F32 or HIPGPT_BF16. */
+int hipgpt_qkv_projection(const float* x, const float* w_qkv,
+                          const float* b_qkv, void* out, int T, int E,
+                          int layout, int out_dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

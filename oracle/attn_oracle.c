@@ -489,3 +489,24 @@ int oracle_mha_backward(const float *grad_out, const float *qkv,
             }
     return 0;
 }
+
+/* ------------------------------------------------------------------ GEMM */
+
+/* matmul_tiled_kernel / matmul_add_bias_tiled_kernel (src/hip_kernels.cpp:
+ * 70-100, :113-143): each output element is one thread's fp32 accumulator,
+ * summed over n = 0..N-1 in order (the 32-wide LDS tiles only stage the
+ * operands; the per-thread order is sequential) with the contracted
+ * `sum += As*Bs` (one fused multiply-add), then `sum + bias[col]`. */
+int oracle_matmul_add_bias(const float *A, const float *B, const float *bias,
+                           float *C, int M, int N, int K)
+{
+    if (M <= 0 || K <= 0) return 0;
+    for (int64_t row = 0; row < M; ++row) {
+        for (int64_t col = 0; col < K; ++col) {
+            float sum = 0.0f;
+            for (int64_t n = 0; n < N; ++n) sum = fmaf(A[row * N + n], B[n * K + col], sum);
+            C[row * K + col] = bias ? sum + bias[col] : sum;
+        }
+    }
+    return 0;
+}

@@ -11,6 +11,8 @@
  *   src/hip_kernels.cpp:329-402  multihead_attention_kernel_fallback -> ORACLE_FALLBACK
  *   src/hip_kernels.cpp:404-451  launch_multihead_attention dispatch
  *                                -> oracle_launch_multihead_attention
+ *   src/hip_kernels.cpp:70-154   launch_matmul / launch_matmul_add_bias
+ *                                -> oracle_matmul_add_bias
  *
  * Pinning (what fixes each function independently of its own formula):
  *   oracle_attention_f64 ........ textbook softmax(QK^T/sqrt(D))V in double;
@@ -27,6 +29,11 @@
  *   oracle_fill_normal .......... SplitMix64 + Box-Muller; pinned by the
  *                                 published SplitMix64 test vector and by
  *                                 moment checks.
+ *   oracle_matmul_add_bias ...... bit-exact against the reference's own
+ *                                matmul kernels (oracle/_ref on an MI355X),
+ *                                exact on integer-valued inputs (every partial
+ *                                sum representable), and within the dot-product
+ *                                error bound of a double-precision product.
  *   Causal mode has no reference counterpart (the reference is non-causal,
  *   src/hip_kernels.cpp:287,:353): it is the reference arithmetic restricted to
  *   keys j <= i + (Sk - Sq), probs written as 0 above the diagonal.  Its last
@@ -114,6 +121,13 @@ void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
 int oracle_mha_backward(const float *grad_out, const float *qkv,
                         const float *probs, float *grad_qkv, int B, int S,
                         int E, int H);
+
+/* Restatement of matmul_add_bias_tiled_kernel (src/hip_kernels.cpp:113-143;
+ * bias == NULL: matmul_tiled_kernel, :70-100): A [M][N], B [N][K], C [M][K]
+ * row-major; C = sequential fmaf sum over n, then + bias[col].  M <= 0 or
+ * K <= 0 writes nothing (the reference's grid is empty).  Returns 0. */
+int oracle_matmul_add_bias(const float *A, const float *B, const float *bias,
+                           float *C, int M, int N, int K);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ __all__ = [
     "ORACLE_SO", "REF_SO", "FLASH", "FALLBACK", "splitmix64", "fill_normal",
     "round_bf16", "attention", "launch_multihead_attention", "ref_available",
     "ref_lib", "planar_qkv", "seeded_planar", "seeded_bshd", "scaled_dot_product",
-    "softmax_rows", "attention_weighted_sum", "mha_backward",
+    "softmax_rows", "attention_weighted_sum", "mha_backward", "matmul_add_bias",
 ]
 
 
@@ -67,6 +67,8 @@ def _oracle():
         L.oracle_softmax_rows.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3
         L.oracle_mha_backward.restype = ctypes.c_int
         L.oracle_mha_backward.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4
+        L.oracle_matmul_add_bias.restype = ctypes.c_int
+        L.oracle_matmul_add_bias.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3
         L.oracle_launch_multihead_attention.restype = ctypes.c_int
         L.oracle_launch_multihead_attention.argtypes = [
             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -197,6 +199,19 @@ def mha_backward(grad_out, qkv, probs, B, S, E, H):
     return out
 
 
+def matmul_add_bias(A, Bm, bias, M, N, K):
+    """Restatement of launch_matmul_add_bias / launch_matmul
+    (src/hip_kernels.cpp:70-154): A [M, N] times B [N, K] (+ bias [K]),
+    sequential fused multiply-add over n.  Returns C [M, K] float32."""
+    A = np.ascontiguousarray(A, dtype=np.float32).reshape(M, N)
+    Bm = np.ascontiguousarray(Bm, dtype=np.float32).reshape(N, K)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).reshape(K)
+    out = np.zeros((M, K), dtype=np.float32)
+    _oracle().oracle_matmul_add_bias(A.ctypes.data, Bm.ctypes.data, None if b is None else b.ctypes.data,
+                                     out.ctypes.data, M, N, K)
+    return out
+
+
 def planar_qkv(qkv, B, S, E, H):
     """[B, S, H, D] views of the Q, K, V planes of a planar buffer."""
     D = E // H
@@ -243,7 +258,9 @@ def ref_lib():
         f.restype = None
         f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4
         L.backward = f
-        for attr, sym, nargs in (("sdp", "_Z25launch_scaled_dot_productPKfS0_Pfiii", (3, 3)),
+        for attr, sym, nargs in (("matmul", "_Z13launch_matmulPKfS0_Pfiii", (3, 3)),
+                                 ("matmul_add_bias", "_Z22launch_matmul_add_biasPKfS0_S0_Pfiii", (4, 3)),
+                                 ("sdp", "_Z25launch_scaled_dot_productPKfS0_Pfiii", (3, 3)),
                                  ("softmax", "_Z14launch_softmaxPKfPfii", (2, 2)),
                                  ("wsum", "_Z29launch_attention_weighted_sumPKfS0_Pfiii", (3, 3))):
             f = getattr(L, sym)

@@ -28,7 +28,8 @@ def test_headers_declare_expected_entry_points():
     assert set(_lib.SIGNATURES) == c_api
     assert declared_functions(HEADERS[0]) == {"launch_multihead_attention", "launch_scaled_dot_product",
                                                "launch_softmax", "launch_attention_weighted_sum",
-                                               "launch_multihead_attention_backward"}
+                                               "launch_multihead_attention_backward", "launch_matmul",
+                                               "launch_matmul_add_bias"}
 
 
 def test_library_exports_every_declared_symbol():
@@ -65,6 +66,20 @@ def test_strerror_and_host_validation():
     assert L.hipgpt_attn_bwd_workspace_bytes(2, 8, 3) == 2 * 3 * 8 * 4
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 64, 2, 0, None, 0, None) == _lib.ERR_WORKSPACE
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 63, 2, 0, p, 1 << 20, None) == _lib.ERR_INVALID
+    # GEMM: bad sizes, strides, segment split and dtype are rejected host-side
+    gemm = L.hipgpt_gemm_bias
+    assert gemm(p, p, None, None, 4, 4, 4, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID   # no output
+    assert gemm(p, p, None, p, 0, 4, 4, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID      # M = 0
+    assert gemm(p, p, None, p, 4, 4, -1, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID     # K < 0
+    assert gemm(None, p, None, p, 4, 4, 4, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID   # no A with K > 0
+    assert gemm(p, p, None, p, 4, 4, 8, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID      # lda < K
+    assert gemm(p, p, None, p, 4, 8, 4, 4, 4, 8, 8, 0, 0, None) == _lib.ERR_INVALID      # ldw < N
+    assert gemm(p, p, None, p, 4, 8, 4, 4, 8, 8, 9, 0, 0, None) == _lib.ERR_INVALID      # seg_w > N
+    assert gemm(p, p, None, p, 4, 8, 4, 4, 8, 2, 4, 0, 0, None) == _lib.ERR_INVALID      # ldc < seg_w
+    assert gemm(p, p, None, p, 4, 8, 4, 4, 8, 8, 8, -1, 0, None) == _lib.ERR_INVALID     # seg_stride < 0
+    assert gemm(p, p, None, p, 4, 8, 4, 4, 8, 8, 8, 0, 5, None) == _lib.ERR_INVALID      # dtype
+    assert L.hipgpt_qkv_projection(p, p, p, p, 4, 8, 2, 0, None) == _lib.ERR_INVALID     # layout
+    assert L.hipgpt_qkv_projection(p, p, p, p, 0, 8, 0, 0, None) == _lib.ERR_INVALID     # T = 0
 
 
 @pytest.mark.parametrize("sym", ["hipgpt_launch_multihead_attention", "_Z26launch_multihead_attentionPKfPfS1_iiii",
