@@ -35,6 +35,8 @@ CONFIGS = {
     "c3_bf16": (8, 12, 1024, 1024, 64, True, "bf16", False, "fwd"),
     "c4": (4, 16, 2048, 2048, 128, True, "f32", False, "fwd"),
     "c5": (64, 12, 1, 2048, 64, False, "f32", False, "decode"),
+    # c5 as a KV-cache step: 2047 cached rows + the new one appended in place
+    "c5_kvcache": (64, 12, 1, 2048, 64, False, "f32", False, "kvcache"),
     # HipGPT's unfused single-head helpers (include/hip_kernels.h:44-46) at the
     # c1 shape with batch and heads merged (B*H = 256 sequences of 256 x 32).
     "a8_scores": (256, 1, 256, 256, 32, False, "f32", False, "sdp"),
@@ -74,6 +76,10 @@ def work(cfg):
         # Q, K, V, dO; write dQ, dK, dV
         pairs = Sq * (Sq + 1) // 2 if causal else Sq * Sk
         return 8.0 * B * H * D * pairs, 4 * B * H * (pairs + 7 * Sq * D)
+    if kind == "kvcache":
+        # read the 2047 cached rows and the new row, q; write the new row into
+        # the cache and O
+        return 4.0 * B * H * D * Sk, 4 * B * H * D * (2 * (Sk - 1) + 2 + 1 + 2 + 1)
     if kind == "decode":
         pairs = Sk
     elif causal:
@@ -102,6 +108,17 @@ def make_call(cfg, torch, A, dev):
         ns = A.decode_default_splits(B, H, Sk)
         ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
         return lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws), {"splits": ns}
+    if kind == "kvcache":
+        kc = torch.randn(B, Sk, H, D, device=dev, generator=g)
+        vc = torch.randn(B, Sk, H, D, device=dev, generator=g)
+        q, kn, vn = torch.randn(3, B, H, D, device=dev, generator=g)
+        out = torch.empty(B, H, D, device=dev)
+        lens = torch.full((B,), Sk - 1, dtype=torch.int32, device=dev)
+        ns = A.decode_default_splits(B, H, Sk)
+        ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
+        # advance=False: every timed call is the same step (row Sk-1 rewritten)
+        return (lambda: A.decode_kvcache(q, kn, vn, kc, vc, lens, out=out, advance=False, num_splits=ns,
+                                         workspace=ws), {"splits": ns, "entry": "hipgpt_attn_decode_kvcache"})
     if kind == "gemm":
         from hipgpt_amd import projection as P
 

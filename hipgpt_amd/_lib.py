@@ -49,6 +49,10 @@ SIGNATURES = {
         + [_i64] * 12
         + [_f, _int, _int, _vp],
     ),
+    "hipgpt_attn_decode_kvcache": (
+        _int,
+        [_vp] * 7 + [_int] * 4 + [_i64] * 11 + [_f, _int, _int, _vp, ctypes.c_size_t, _vp],
+    ),
     "hipgpt_launch_matmul": (None, [_vp, _vp, _vp, _int, _int, _int]),
     "hipgpt_launch_matmul_add_bias": (None, [_vp, _vp, _vp, _vp, _int, _int, _int]),
     "hipgpt_gemm_bias": (

@@ -10,6 +10,8 @@ provider here); every call goes through the C ABI to the HIP kernels.
 * :func:`attention` -- strided ``[B, S, H, D]`` views, fp32 or bf16 inputs.
 * :func:`decode` -- one query row per sequence against ``kv_len`` keys,
   split-KV.
+* :func:`decode_kvcache` -- one KV-cached generation step: append the new
+  key/value row at each sequence's device-side length, attend, advance.
 """
 from __future__ import annotations
 
@@ -228,6 +230,55 @@ def decode(q, k, v, out=None, num_splits=None, workspace=None, scale=None, strea
         sc, ns, _ptr(workspace), ws_bytes, _stream(stream),
     )
     _lib.check(rc, "hipgpt_attn_decode")
+    return out
+
+
+def _bhd_strides(t, name, B, H, D):
+    if tuple(t.shape) != (B, H, D) or t.stride(2) != 1:
+        raise ValueError(f"{name} must be [B, H, D] with contiguous D")
+    return t.stride(0), t.stride(1)
+
+
+def decode_kvcache(q, k_new, v_new, k_cache, v_cache, lens, out=None, advance=True, num_splits=None,
+                   workspace=None, scale=None, stream=None):
+    """One KV-cached decode step over sequences of different lengths.
+
+    q, k_new, v_new: [B, H, D] fp32 (the step's projections); k_cache,
+    v_cache: [B, max_len, H, D] fp32 with the same strides; lens: int32
+    device tensor [B] of cached rows.  Writes k_new / v_new at row lens[b],
+    attends q over the lens[b] + 1 rows and (``advance``) increments lens on
+    the device.  Sequences at capacity get NaN and are left unchanged.
+    """
+    for name, t in (("q", q), ("k_new", k_new), ("v_new", v_new), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _need_cuda(name, t, torch.float32)
+    _need_cuda("lens", lens, torch.int32)
+    B, H, D = q.shape
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2] != H or k_cache.shape[3] != D:
+        raise ValueError("k_cache must be [B, max_len, H, D]")
+    if v_cache.shape != k_cache.shape or v_cache.stride() != k_cache.stride() or k_cache.stride(3) != 1:
+        raise ValueError("v_cache must match k_cache in shape and strides, D contiguous")
+    if lens.numel() != B or not lens.is_contiguous():
+        raise ValueError("lens must be a contiguous int32 tensor of B elements")
+    max_len = k_cache.shape[1]
+    if out is None:
+        out = torch.empty((B, H, D), device=q.device, dtype=torch.float32)
+    _need_cuda("out", out, torch.float32)
+    qs = _bhd_strides(q, "q", B, H, D)
+    ks = _bhd_strides(k_new, "k_new", B, H, D)
+    vs = _bhd_strides(v_new, "v_new", B, H, D)
+    os_ = _bhd_strides(out, "out", B, H, D)
+    ns = decode_default_splits(B, H, max_len) if num_splits is None else int(num_splits)
+    ns = max(1, min(ns, max_len))
+    need = decode_workspace_bytes(B, H, D, ns)
+    if workspace is None and need > 0:
+        workspace = torch.empty(need // 4, device=q.device, dtype=torch.float32)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    sc = -1.0 if scale is None else float(scale)
+    rc = _lib.lib().hipgpt_attn_decode_kvcache(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(lens), _ptr(out),
+        B, H, D, max_len, *qs, *ks, *vs, k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), *os_,
+        sc, ns, int(bool(advance)), _ptr(workspace), ws_bytes, _stream(stream))
+    _lib.check(rc, "hipgpt_attn_decode_kvcache")
     return out
 
 

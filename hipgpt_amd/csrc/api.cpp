@@ -358,6 +358,57 @@ int hipgpt_attn_decode(const float* q, const float* k, const float* v, float* o,
     return from_hip(hipgpt::launch_decode(a, hipgpt::kF32, ns, static_cast<float*>(workspace), stream));
 }
 
+int hipgpt_attn_decode_kvcache(const float* q, const float* k_new, const float* v_new, float* k_cache,
+                               float* v_cache, int* lens, float* o, int B, int H, int D, int max_len, int64_t q_bs,
+                               int64_t q_hs, int64_t kn_bs, int64_t kn_hs, int64_t vn_bs, int64_t vn_hs, int64_t c_bs,
+                               int64_t c_ts, int64_t c_hs, int64_t o_bs, int64_t o_hs, float scale, int num_splits,
+                               int advance, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!q || !k_new || !v_new || !k_cache || !v_cache || !lens || !o || B <= 0 || H <= 0 || D <= 0 ||
+        max_len <= 0 || !std::isfinite(scale))
+        return HIPGPT_ERR_INVALID;
+    if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if (!hipgpt::decode_supported(D, hipgpt::kF32)) return HIPGPT_ERR_UNSUPPORTED;
+    const bool ok = aligned16(q) && aligned16(k_new) && aligned16(v_new) && aligned16(k_cache) &&
+                    aligned16(v_cache) && q_bs % 4 == 0 && q_hs % 4 == 0 && kn_bs % 4 == 0 && kn_hs % 4 == 0 &&
+                    vn_bs % 4 == 0 && vn_hs % 4 == 0 && c_bs % 4 == 0 && c_ts % 4 == 0 && c_hs % 4 == 0;
+    if (!ok) return HIPGPT_ERR_UNSUPPORTED;
+    int ns = num_splits > 0 ? num_splits : hipgpt::decode_default_splits(B, H, max_len);
+    if (ns > max_len) ns = max_len;
+    const size_t need = hipgpt_attn_decode_workspace_bytes(B, H, D, ns);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return HIPGPT_ERR_WORKSPACE;
+    AttnArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.o = o;
+    a.q_bs = q_bs;
+    a.q_hs = q_hs;
+    a.k_bs = a.v_bs = c_bs;
+    a.k_ts = a.v_ts = c_ts;
+    a.k_hs = a.v_hs = c_hs;
+    a.o_bs = o_bs;
+    a.o_hs = o_hs;
+    a.B = B;
+    a.H = H;
+    a.Sq = 1;
+    a.Sk = max_len;
+    a.D = D;
+    a.qscale = default_scale(D, scale) * hipgpt::kLog2e;
+    hipgpt::KvcArgs kc{};
+    kc.k_new = k_new;
+    kc.v_new = v_new;
+    kc.kn_bs = kn_bs;
+    kc.kn_hs = kn_hs;
+    kc.vn_bs = vn_bs;
+    kc.vn_hs = vn_hs;
+    kc.kc = k_cache;
+    kc.vc = v_cache;
+    kc.lens = lens;
+    kc.max_len = max_len;
+    kc.advance = advance ? 1 : 0;
+    return from_hip(hipgpt::launch_decode(a, hipgpt::kF32, ns, static_cast<float*>(workspace), stream, &kc));
+}
+
 void hipgpt_launch_matmul(const float* A, const float* B, float* C, int M, int N, int K) {
     launch_matmul(A, B, C, M, N, K);
 }

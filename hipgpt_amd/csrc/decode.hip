@@ -15,6 +15,17 @@
 //     merged through LDS at the end.  With one split the result is final.
 //   * reduce kernel: merges the splits' (m, l, O) with the log-sum-exp rule
 //       M = max m_s,  L = sum l_s 2^(m_s - M),  O = sum O_s 2^(m_s - M) / L.
+//
+// KV-cache mode (KVC): K/V are a cache [B][max_len][H][D] with a device
+// length lens[b] per sequence; the step's own key/value row (k_new, v_new)
+// sits at position lens[b].  Splits cover the lens[b] + 1 visible keys of
+// their sequence; the split that owns position lens[b] takes that row from
+// k_new / v_new and writes it into the cache (no other workgroup touches
+// that cache row, so there is no race).  A sequence whose length is outside
+// [0, max_len) is left untouched and its output is NaN (the partial sum is
+// poisoned, so the reduce propagates it).  lens[b] is advanced by the reduce
+// kernel's workgroup for head 0 -- reduce workgroups never read lens -- or,
+// with one split, by a one-thread-per-sequence kernel after the step.
 #include "common.h"
 #include "kernels.h"
 
@@ -24,8 +35,8 @@ namespace {
 
 constexpr int DEC_NW = 4;  // waves per workgroup
 
-template <int DP, int U>
-__global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a, int nsplit, int chunk,
+template <int DP, int U, bool KVC>
+__global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a, KvcArgs kc, int nsplit, int chunk,
                                                                      float* ws) {
     constexpr int LPK = DP / 4;   // lanes per key row
     constexpr int KPW = 64 / LPK; // key rows per wave per load
@@ -44,8 +55,21 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a,
     const int bh = blockIdx.x % BH;
     const int split = blockIdx.x / BH;
     const int b = bh / a.H, h = bh % a.H;
-    const int k0 = split * chunk;
-    const int k1 = min(a.Sk, k0 + chunk);
+    int k0 = split * chunk;
+    int k1 = min(a.Sk, k0 + chunk);
+    int len = 0;        // KVC: cached rows before the new one
+    bool bad = false;   // KVC: length outside [0, max_len)
+    bool owns_new = false;
+    if (KVC) {
+        len = kc.lens[b];
+        bad = len < 0 || len >= kc.max_len;
+        const int kv = bad ? 0 : len + 1;
+        const int ch = (kv + nsplit - 1) / nsplit;
+        k0 = split * ch;
+        k1 = min(kv, k0 + ch);
+        owns_new = k0 <= len && len < k1;
+        if (owns_new) k1 = len;  // cache rows only; the new row is added below
+    }
 
     const float* qp = static_cast<const float*>(a.q) + b * a.q_bs + h * a.q_hs;
     const float* Kp = static_cast<const float*>(a.k) + b * a.k_bs + h * a.k_hs + sub * 4;
@@ -100,6 +124,34 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a,
         m = m_new;
     }
 
+    if (KVC && owns_new) {
+        // the step's own key/value row: into the online softmax of group 0
+        // of wave 0 (lanes 0..LPK-1) and into the cache at position len
+        const float* kn = kc.k_new + b * kc.kn_bs + h * kc.kn_hs + sub * 4;
+        const float* vn = kc.v_new + b * kc.vn_bs + h * kc.vn_hs + sub * 4;
+        floatx4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
+        if (tid < LPK) {
+            kv4 = *reinterpret_cast<const floatx4*>(kn);
+            vv4 = *reinterpret_cast<const floatx4*>(vn);
+            *reinterpret_cast<floatx4*>(kc.kc + b * a.k_bs + (int64_t)len * a.k_ts + h * a.k_hs + sub * 4) = kv4;
+            *reinterpret_cast<floatx4*>(kc.vc + b * a.v_bs + (int64_t)len * a.v_ts + h * a.v_hs + sub * 4) = vv4;
+        }
+        float d = q4[0] * kv4[0];
+        d = fmaf(q4[1], kv4[1], d);
+        d = fmaf(q4[2], kv4[2], d);
+        d = fmaf(q4[3], kv4[3], d);
+#pragma unroll
+        for (int msk = LPK / 2; msk >= 1; msk >>= 1) d += __shfl_xor(d, msk);
+        if (slot == 0) {
+            const float m_new = fmaxf(m, d);
+            const float alpha = fast_exp2(m - m_new);
+            const float p = fast_exp2(d - m_new);
+            l = fmaf(l, alpha, p);
+            o4 = o4 * alpha + p * vv4;
+            m = m_new;
+        }
+    }
+
     if (sub == 0) {
         s_ml[slot][0] = m;
         s_ml[slot][1] = l;
@@ -119,8 +171,9 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a,
             L = fmaf(s_ml[g][1], w, L);
             O = fmaf(s_o[g][d], w, O);
         }
+        if (KVC && bad) L = O = __builtin_nanf("");  // poisons this (b, h): output NaN
         if (nsplit == 1) {
-            if (d < a.D) a.o[b * a.o_bs + h * a.o_hs + d] = O / fmaxf(L, 1e-20f);
+            if (d < a.D) a.o[b * a.o_bs + h * a.o_hs + d] = KVC && bad ? O : O / fmaxf(L, 1e-20f);
         } else {
             float* wml = ws + ((int64_t)bh * nsplit + split) * 2;
             float* wo = ws + (int64_t)BH * nsplit * 2 + ((int64_t)bh * nsplit + split) * DP;
@@ -134,10 +187,17 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a,
 }
 
 template <int DP>
-__global__ __launch_bounds__(64) void decode_reduce_kernel(AttnArgs a, int nsplit, const float* ws) {
+__global__ __launch_bounds__(64) void decode_reduce_kernel(AttnArgs a, int nsplit, const float* ws, int* advance_lens,
+                                                           int max_len) {
     const int bh = blockIdx.x;
     const int BH = a.B * a.H;
     const int b = bh / a.H, h = bh % a.H;
+    // KV-cache step: the head-0 workgroup advances its sequence (no reduce
+    // workgroup reads lens, and the partial kernel has completed)
+    if (advance_lens && h == 0 && threadIdx.x == 0) {
+        const int n = advance_lens[b];
+        if (n >= 0 && n < max_len) advance_lens[b] = n + 1;
+    }
     const float* wml = ws + (int64_t)bh * nsplit * 2;
     const float* wo = ws + (int64_t)BH * nsplit * 2 + (int64_t)bh * nsplit * DP;
     float M = kMaxInit;
@@ -152,25 +212,46 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(AttnArgs a, int nspli
     }
 }
 
+__global__ __launch_bounds__(256) void kvc_advance_kernel(int* lens, int B, int max_len) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b < B) {
+        const int n = lens[b];
+        if (n >= 0 && n < max_len) lens[b] = n + 1;
+    }
+}
+
 int decode_padded_dim(int D) {
     if (D == 32 || D == 64 || D == 128 || D == 256) return D;
     return 0;
 }
 
 template <int DP>
-hipError_t launch_decode_dp(const AttnArgs& a, int nsplit, float* ws, hipStream_t stream) {
+hipError_t launch_decode_dp(const AttnArgs& a, const KvcArgs* kc, int nsplit, float* ws, hipStream_t stream) {
     constexpr int U = DP >= 128 ? 4 : 8;
     const int BH = a.B * a.H;
     const int chunk = (a.Sk + nsplit - 1) / nsplit;
     const int64_t grid = (int64_t)BH * nsplit;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((decode_partial_kernel<DP, U>), dim3((unsigned)grid), dim3(DEC_NW * 64), 0, stream, a,
-                       nsplit, chunk, ws);
+    if (kc)
+        hipLaunchKernelGGL((decode_partial_kernel<DP, U, true>), dim3((unsigned)grid), dim3(DEC_NW * 64), 0, stream, a,
+                           *kc, nsplit, chunk, ws);
+    else
+        hipLaunchKernelGGL((decode_partial_kernel<DP, U, false>), dim3((unsigned)grid), dim3(DEC_NW * 64), 0, stream,
+                           a, KvcArgs{}, nsplit, chunk, ws);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || nsplit == 1) return e;
-    hipLaunchKernelGGL((decode_reduce_kernel<DP>), dim3((unsigned)BH), dim3(64), 0, stream, a, nsplit,
-                       static_cast<const float*>(ws));
-    return hipGetLastError();
+    if (e != hipSuccess) return e;
+    int* adv = kc && kc->advance ? kc->lens : nullptr;
+    const int max_len = kc ? kc->max_len : 0;
+    if (nsplit > 1) {
+        hipLaunchKernelGGL((decode_reduce_kernel<DP>), dim3((unsigned)BH), dim3(64), 0, stream, a, nsplit,
+                           static_cast<const float*>(ws), adv, max_len);
+        e = hipGetLastError();
+    } else if (adv) {
+        hipLaunchKernelGGL(kvc_advance_kernel, dim3((unsigned)((a.B + 255) / 256)), dim3(256), 0, stream, adv, a.B,
+                           max_len);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 }  // namespace
@@ -186,14 +267,15 @@ int decode_default_splits(int B, int H, int kv_len) {
     return n;
 }
 
-hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream) {
+hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream,
+                         const KvcArgs* kc) {
     if (!decode_supported(a.D, dtype) || nsplit < 1) return hipErrorInvalidValue;
     if (nsplit > 1 && ws == nullptr) return hipErrorInvalidValue;
     switch (decode_padded_dim(a.D)) {
-        case 32: return launch_decode_dp<32>(a, nsplit, ws, stream);
-        case 64: return launch_decode_dp<64>(a, nsplit, ws, stream);
-        case 128: return launch_decode_dp<128>(a, nsplit, ws, stream);
-        case 256: return launch_decode_dp<256>(a, nsplit, ws, stream);
+        case 32: return launch_decode_dp<32>(a, kc, nsplit, ws, stream);
+        case 64: return launch_decode_dp<64>(a, kc, nsplit, ws, stream);
+        case 128: return launch_decode_dp<128>(a, kc, nsplit, ws, stream);
+        case 256: return launch_decode_dp<256>(a, kc, nsplit, ws, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -12,21 +12,21 @@
 // (N = 3E, seg_w = E, seg_stride = M*E), the planar [Q|K|V] buffer the
 // attention launcher reads.  Output fp32 or bf16 (RNE).
 //
-// Tiling: a workgroup owns a BM x BN tile of C and walks K in steps of 32.
+// Tiling: a workgroup owns a BM x BN tile of C and walks K in steps of GBK.
 // Each wave computes a WM x WN sub-tile as C^T = W^T A^T on
 // v_mfma_f32_32x32x2_f32, so an accumulator register group holds four
 // consecutive output columns of one row (16-byte stores, 16-byte bias loads).
 // Operand staging: global -> registers -> LDS, double buffered, one barrier
 // per k-tile; the next tile's global loads are in flight during the MFMAs.
-//   A tile [BM][32] (pitch 36 floats): lane (c, h) reads row c, k = 16h + s as
-//     ds_read_b128 (four k-steps per read).
-//   W tile [32][BN] (pitch BN+4, second half of the k rows shifted by 32
+//   A tile [BM][GBK] (pitch GBK+4 floats): lane (c, h) reads row c,
+//     k = (GBK/2)h + s as ds_read_b128 (four k-steps per read).
+//   W tile [GBK][BN] (pitch BN+4, second half of the k rows shifted by 32
 //     floats so the two lane halves read different banks): lane (c, h) reads
-//     W[16h + s][c] as one dword per k-step.
+//     W[(GBK/2)h + s][c] as one dword per k-step.
 // MFMA 32x32x2 f32 operand layout (lane l, c = l & 31, h = l >> 5): A-operand
 // value = row c of the MFMA's M dim, B-operand value = column c of its N dim,
-// both at contraction index h of the step; here contraction index k = 16h + s
-// at step s, the same bijection for both operands.
+// both at contraction index h of the step; here contraction index
+// k = (GBK/2)h + s at step s, the same bijection for both operands.
 #include "common.h"
 #include "kernels.h"
 
@@ -34,11 +34,11 @@ namespace hipgpt {
 
 namespace {
 
-constexpr int GBK = 32;         // k per tile
-constexpr int APITCH = GBK + 4; // A tile row pitch, floats
-
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int GBK_ = 32>
 struct Cfg {
+    static constexpr int GBK = GBK_;         // k per tile
+    static constexpr int APITCH = GBK + 4;   // A tile row pitch, floats
+    static constexpr int ACPR = GBK / 4;     // 16-byte chunks per A tile row
     static constexpr int WAVES_M = BM / WM;
     static constexpr int WAVES_N = BN / WN;
     static constexpr int NW = WAVES_M * WAVES_N;
@@ -55,15 +55,18 @@ struct Cfg {
     static constexpr int W_PER = W_CHUNKS / NT;
     static_assert(A_CHUNKS % NT == 0 && W_CHUNKS % NT == 0, "tile loads must split evenly over the workgroup");
     static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % WM == 0 && BN % WN == 0, "bad tile shape");
-    // W row r of the tile lives at r * WPITCH + (r >= 16 ? 32 : 0).
-    __device__ __forceinline__ static int wrow(int r) { return r * WPITCH + ((r >> 4) << 5); }
+    // W row r of the tile lives at r * WPITCH + (r >= GBK/2 ? 32 : 0).
+    __device__ __forceinline__ static int wrow(int r) { return r * WPITCH + (r >= GBK / 2 ? 32 : 0); }
 };
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
-template <int BM, int BN, int WM, int WN, bool VEC, bool BF16OUT>
+template <int BM, int BN, int WM, int WN, int GBK, int NACC, bool VEC, bool BF16OUT>
 __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(GemmArgs g) {
-    using C = Cfg<BM, BN, WM, WN>;
+    using C = Cfg<BM, BN, WM, WN, GBK>;
+    constexpr int APITCH = C::APITCH;
+    constexpr int ACPR = C::ACPR;
+    constexpr int HS = GBK / 2;  // k-steps per tile (each step takes k = HS*h + s)
     __shared__ __attribute__((aligned(16))) float lds[2 * C::STAGE];
 
     const int tid = threadIdx.x;
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
 #pragma unroll
         for (int i = 0; i < C::A_PER; ++i) {
             const int f = tid + i * C::NT;
-            aoff[i] = (int)(((f >> 3) * g.lda + (f & 7) * 4) * 4);
+            aoff[i] = (int)(((f / ACPR) * g.lda + (f % ACPR) * 4) * 4);
         }
 #pragma unroll
         for (int i = 0; i < C::W_PER; ++i) {
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
 #pragma unroll
         for (int i = 0; i < C::A_PER; ++i) {
             const int f = tid + i * C::NT;
-            const int r = f >> 3, kc = (f & 7) * 4;
+            const int r = f / ACPR, kc = (f % ACPR) * 4;
             if constexpr (VEC) {
                 // rows past M read as zero (buffer range); k past K is masked
                 // here because it would read the next row's values
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
 #pragma unroll
         for (int i = 0; i < C::A_PER; ++i) {
             const int f = tid + i * C::NT;
-            *reinterpret_cast<floatx4*>(st + (f >> 3) * APITCH + (f & 7) * 4) = ar[i];
+            *reinterpret_cast<floatx4*>(st + (f / ACPR) * APITCH + (f % ACPR) * 4) = ar[i];
         }
         float* ws = st + C::A_ELEMS;
 #pragma unroll
@@ -153,26 +156,30 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         }
     };
 
-    floatx16 acc[C::NB][C::MB];
+    // NACC independent accumulator chains per output block (k-steps
+    // alternate between them), summed in the epilogue.
+    floatx16 acc[NACC][C::NB][C::MB];
 #pragma unroll
-    for (int i = 0; i < C::NB; ++i)
+    for (int x = 0; x < NACC; ++x)
 #pragma unroll
-        for (int j = 0; j < C::MB; ++j)
+        for (int i = 0; i < C::NB; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+            for (int j = 0; j < C::MB; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[x][i][j][r] = 0.f;
 
     auto compute = [&](const float* st) {
-        const float* As = st + (wm0 + c) * APITCH + h * 16;
+        const float* As = st + (wm0 + c) * APITCH + h * HS;
         const float* Ws = st + C::A_ELEMS + wn0 + c;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < HS / 4; ++q) {
             floatx4 av[C::MB];
 #pragma unroll
             for (int j = 0; j < C::MB; ++j) av[j] = *reinterpret_cast<const floatx4*>(As + j * 32 * APITCH + 4 * q);
             float wv[C::NB][4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int row = C::wrow(h * 16 + 4 * q + u);
+                const int row = C::wrow(h * HS + 4 * q + u);
 #pragma unroll
                 for (int i = 0; i < C::NB; ++i) wv[i][u] = Ws[row + 32 * i];
             }
@@ -182,7 +189,8 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
                 for (int i = 0; i < C::NB; ++i)
 #pragma unroll
                     for (int j = 0; j < C::MB; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wv[i][u], av[j][u], acc[i][j], 0, 0, 0);
+                        acc[u % NACC][i][j] =
+                            __builtin_amdgcn_mfma_f32_32x32x2f32(wv[i][u], av[j][u], acc[u % NACC][i][j], 0, 0, 0);
         }
     };
 
@@ -219,7 +227,12 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
                 if (m >= g.M) continue;
                 floatx4 v;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = acc[i][j][4 * q + u] + bv[u];
+                for (int u = 0; u < 4; ++u) {
+                    float t = acc[0][i][j][4 * q + u];
+#pragma unroll
+                    for (int x = 1; x < NACC; ++x) t += acc[x][i][j][4 * q + u];
+                    v[u] = t + bv[u];
+                }
                 if (VEC) {
                     if (n >= g.N) continue;
                     const int64_t off = (int64_t)(n / g.seg_w) * g.seg_stride + (int64_t)m * g.ldc + n % g.seg_w;
@@ -248,38 +261,38 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
     }
 }
 
-template <int BM, int BN, int WM, int WN, bool VEC>
+template <int BM, int BN, int WM, int WN, bool VEC, int GBK = 32, int NACC = 1>
 hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
     const int64_t tiles = (int64_t)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (tiles <= 0 || tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
-    constexpr int NT = Cfg<BM, BN, WM, WN>::NT;
+    constexpr int NT = Cfg<BM, BN, WM, WN, GBK>::NT;
     if (g.out_bf16)
-        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, VEC, true>), dim3((unsigned)tiles), dim3(NT), 0, s, g);
+        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, true>), dim3((unsigned)tiles), dim3(NT), 0,
+                           s, g);
     else
-        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, VEC, false>), dim3((unsigned)tiles), dim3(NT), 0, s, g);
+        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, false>), dim3((unsigned)tiles), dim3(NT),
+                           0, s, g);
     return hipGetLastError();
 }
 
-// Tile shape per problem: the 128 x 64 tile when it yields at least two
-// workgroups per CU, else 64 x 64 (more, smaller tiles fill the 256 CUs).
-#ifndef HIPGPT_GEMM_BIG_MIN_TILES
-#define HIPGPT_GEMM_BIG_MIN_TILES 512
-#endif
-
+// One tile shape for every problem: 64 x 128 outputs per workgroup, eight
+// waves of 32 x 32, k-tiles of 32.  Measured on MI355X against 128x64,
+// 64x64, 128x128, 32x64, 64x32 and 128x64/8-wave tiles, k-tiles of 16 and
+// 64 and two accumulator chains: best or within noise on every projection
+// shape of the c1 and c3 layers (the kernel is latency-bound, so more
+// resident waves beat larger per-wave tiles).
 template <bool VEC>
 hipError_t launch_vec(const GemmArgs& g, hipStream_t s) {
-    const int64_t big = (int64_t)((g.M + 127) / 128) * ((g.N + 63) / 64);
-    if (big >= HIPGPT_GEMM_BIG_MIN_TILES) return launch_cfg<128, 64, 64, 32, VEC>(g, s);
-    return launch_cfg<64, 64, 32, 32, VEC>(g, s);
+    return launch_cfg<64, 128, 32, 32, VEC>(g, s);
 }
 
 }  // namespace
 
 bool gemm_vec_ok(const GemmArgs& g) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    // 32-bit buffer offsets: W rows up to K + 32, A rows up to 128 past a tile's first row
-    const int64_t wbytes = ((int64_t)(g.K + GBK) * g.ldw + 128) * 4;
-    const int64_t abytes = ((int64_t)128 * g.lda + g.K + 2 * GBK) * 4;
+    // 32-bit buffer offsets: W rows up to K + 64, A rows up to 128 past a tile's first row
+    const int64_t wbytes = ((int64_t)(g.K + 64) * g.ldw + 128) * 4;
+    const int64_t abytes = ((int64_t)128 * g.lda + g.K + 128) * 4;
     return al(g.A) && al(g.W) && al(g.C) && (!g.bias || al(g.bias)) && g.K % 4 == 0 && g.N % 4 == 0 &&
            g.lda % 4 == 0 && g.ldw % 4 == 0 && g.ldc % 4 == 0 && g.seg_w % 4 == 0 && g.seg_stride % 4 == 0 &&
            wbytes < ((int64_t)1 << 31) && abytes < ((int64_t)1 << 31);

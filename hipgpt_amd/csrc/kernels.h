@@ -21,11 +21,26 @@ hipError_t launch_fa_bf16(const AttnArgs& a, bool causal, hipStream_t stream);
 // Any head dim, fp32: one wave per query row (the path for D > 128).
 hipError_t launch_attn_generic_f32(const AttnArgs& a, bool causal, hipStream_t stream);
 
+// KV-cache decode step: the cache is a.k / a.v (with a.k_* / a.v_* strides,
+// a.Sk = max_len); the new row of sequence b is appended at lens[b].
+struct KvcArgs {
+    const float* k_new;
+    const float* v_new;
+    int64_t kn_bs, kn_hs, vn_bs, vn_hs;
+    float* kc;  // writable views of the caches (same memory as a.k / a.v)
+    float* vc;
+    int* lens;  // device [B]
+    int max_len;
+    int advance;  // increment lens[b] after the step
+};
+
 // Split-KV single-query decode.  q: [B][1][H*D]-style strides in a; partial
 // results go to ws (nsplit * B * H * (D + 2) floats) when nsplit > 1.
+// kc != null selects the KV-cache step.
 bool decode_supported(int D, int dtype);
 int decode_default_splits(int B, int H, int kv_len);
-hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream);
+hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hipStream_t stream,
+                         const KvcArgs* kc = nullptr);
 
 // Attention backward on the forward's probs (HipGPT src/hip_kernels.cpp:1159-1272).
 // All [B][S][H][D] tensors share one (batch, token, head) stride set; dvec is

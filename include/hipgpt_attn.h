@@ -108,6 +108,34 @@ int hipgpt_attn_decode(const float* q, const float* k, const float* v,
                        float scale, int num_splits, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
 
+/* One KV-cached decode step for a batch of sequences of different lengths
+ * (the step HipGPT's generation loop, src/gpt_model.cpp:261-273, would take
+ * instead of recomputing the whole window per token).
+ *   k_cache, v_cache: [B][max_len][H][D] fp32, element (b, t, h, d) at
+ *     X[b*c_bs + t*c_ts + h*c_hs + d]; rows [0, lens[b]) hold the cached
+ *     keys / values of sequence b.
+ *   lens: device int32 [B], read on the device (no host synchronisation).
+ *   q, k_new, v_new, o: the step's rows [B][H][D] with (bs, hs) strides.
+ * The step writes k_new / v_new into row lens[b] of the caches, computes
+ * o = softmax(q K^T * scale) V over the lens[b] + 1 rows, and, when advance
+ * is non-zero, increments lens[b].  A sequence with lens[b] < 0 or
+ * lens[b] >= max_len is left unchanged and gets a NaN output.  Split-KV as
+ * hipgpt_attn_decode (num_splits <= 0 picks the default for max_len; the
+ * workspace is hipgpt_attn_decode_workspace_bytes(B, H, D, splits)).  fp32,
+ * D in {32, 64, 128, 256}, 16-byte aligned rows.  Rows past lens[b] + 1 are
+ * never read. */
+int hipgpt_attn_decode_kvcache(const float* q, const float* k_new,
+                               const float* v_new, float* k_cache,
+                               float* v_cache, int* lens, float* o, int B,
+                               int H, int D, int max_len,
+                               int64_t q_bs, int64_t q_hs,
+                               int64_t kn_bs, int64_t kn_hs,
+                               int64_t vn_bs, int64_t vn_hs,
+                               int64_t c_bs, int64_t c_ts, int64_t c_hs,
+                               int64_t o_bs, int64_t o_hs, float scale,
+                               int num_splits, int advance, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
 /* ---- projections either side of the attention (fp32 MFMA GEMM) ---- */
 
 /* C-linkage twins of launch_matmul / launch_matmul_add_bias

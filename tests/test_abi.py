@@ -66,6 +66,14 @@ def test_strerror_and_host_validation():
     assert L.hipgpt_attn_bwd_workspace_bytes(2, 8, 3) == 2 * 3 * 8 * 4
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 64, 2, 0, None, 0, None) == _lib.ERR_WORKSPACE
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 63, 2, 0, p, 1 << 20, None) == _lib.ERR_INVALID
+    # KV-cache decode: null lens / caches, bad sizes, unsupported D, missing workspace
+    kvc = L.hipgpt_attn_decode_kvcache
+    z11 = [0] * 11
+    assert kvc(p, p, p, p, p, None, p, 2, 2, 64, 16, *z11, -1.0, 1, 1, None, 0, None) == _lib.ERR_INVALID
+    assert kvc(p, p, p, None, p, p, p, 2, 2, 64, 16, *z11, -1.0, 1, 1, None, 0, None) == _lib.ERR_INVALID
+    assert kvc(p, p, p, p, p, p, p, 2, 2, 64, 0, *z11, -1.0, 1, 1, None, 0, None) == _lib.ERR_INVALID
+    assert kvc(p, p, p, p, p, p, p, 2, 2, 48, 16, *z11, -1.0, 1, 1, None, 0, None) == _lib.ERR_UNSUPPORTED
+    assert kvc(p, p, p, p, p, p, p, 2, 2, 64, 4096, *z11, -1.0, 8, 1, None, 0, None) == _lib.ERR_WORKSPACE
     # GEMM: bad sizes, strides, segment split and dtype are rejected host-side
     gemm = L.hipgpt_gemm_bias
     assert gemm(p, p, None, None, 4, 4, 4, 4, 4, 4, 4, 0, 0, None) == _lib.ERR_INVALID   # no output
