@@ -16,6 +16,34 @@ namespace fa {
 constexpr int BK = 32;  // keys per tile
 constexpr int QW = 32;  // queries per wave
 
+// Rescale threshold of the online softmax (log2 units): the running max of a
+// row is only raised when a tile's max exceeds it by more than this, so the
+// O / l rescale is skipped on most tiles; exponentiated scores are then at
+// most 2^kLazyMax, far from fp32 overflow, and the final O / l is unchanged.
+constexpr float kLazyMax = 8.0f;
+
+// SIMD of the calling wave (HW_ID.SIMD_ID, bits [5:4]).
+__device__ __forceinline__ int wave_simd() { return (__builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11))) & 3; }
+
+// The hardware places a workgroup's waves on the CU's SIMDs in an order that
+// varies between workgroups.  Rank each wave by its SIMD (ties by wave id):
+// a bijection onto 0..NW-1 that, with one wave per SIMD, is the SIMD id, so
+// that roles rotated by the workgroup's launch rank spread causal work evenly
+// over the SIMDs.  One barrier; `slots` is NW ints of LDS.
+template <int NW>
+__device__ __forceinline__ int simd_rank(int* slots, int wave, int lane) {
+    const int me = wave_simd();
+    if (lane == 0) slots[wave] = me;
+    __syncthreads();
+    int rk = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const int s = slots[w];
+        rk += (s < me) || (s == me && w < wave);
+    }
+    return __builtin_amdgcn_readfirstlane(rk);
+}
+
 // Key (within the tile) held by accumulator register r of lane half h.
 __device__ __forceinline__ int acc_key(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 

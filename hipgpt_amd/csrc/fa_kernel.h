@@ -130,21 +130,22 @@ struct FaKernel {
         }
     };
 
-    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw) {
+    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int* simd_slots) {
         E* const lds = reinterpret_cast<E*>(lds_raw);
         const int tid = threadIdx.x;
         const int lane = tid & 63;
-        const int wave = tid >> 6;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31;
         const int hf = lane >> 5;
         const int BH = a.B * a.H;
         const int bh = blockIdx.x % BH;
         const int rank = blockIdx.x / BH;
         const int qb = CAUSAL ? a.n_qblk - 1 - rank : rank;  // longest rows first
-        // Wave w runs on SIMD w % 4.  Rotating the wave -> (sub-block, split)
-        // roles with the launch rank gives each SIMD a different role in
-        // each of the co-resident workgroups, evening out causal work.
-        const int role = (wave + rank) % NW;
+        // Rotating the (sub-block, split) roles with the launch rank over the
+        // waves ranked by SIMD gives each SIMD a different role in each of
+        // the co-resident workgroups, evening out causal work.  Roles are
+        // wave-uniform (scalar registers), so tile indexing stays scalar.
+        const int role = (simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
         const int qs = role / NKS;
         const int ks = role % NKS;
         const int b = bh / a.H;
@@ -188,8 +189,6 @@ struct FaKernel {
         Stager st;
         st.init(Kp, Vp, a.k_ts, a.v_ts, Sk, a.D, tid);
         // ------------------------------------------------------------------
-        // Stage loop.  MODE 0: online softmax + PV.  MODE 1: max/sum only.
-        // MODE 2: probs store + PV with the final (m, l).
         // One stage of compute on LDS buffer (i & 1).  MODE 0: online softmax
         // + PV.  MODE 1: max/sum only.  MODE 2: probs store + PV with the
         // final (m, l).
@@ -202,24 +201,26 @@ struct FaKernel {
             typename TR::VReg vreg;
             if (MODE != 1) TR::load_v(vreg, vt_of(cur, t), c, hf);  // in flight during the softmax
             if (MODE == 0) {
-                const float m_new = vmax(m_run, tile_max(s) * sc);
-                float ls = 0.f;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    s[r] = fast_exp2(fmaf(s[r], sc, -m_new));
-                    ls += s[r];
-                }
-                ls = halves_sum(ls);
-                if (__any(m_new != m_run)) {  // rescale only when a row max moved
+                // lazy rescale: raise the running max only when a row's tile
+                // max exceeds it by more than kLazyMax
+                const float tmax = tile_max(s) * sc;
+                if (__any(tmax > m_run + kLazyMax)) {
+                    const float m_new = vmax(m_run, tmax);
                     const float alpha = fast_exp2(m_run - m_new);
                     l_run *= alpha;
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                    m_run = m_new;
                 }
-                l_run += ls;
-                m_run = m_new;
+                float ls = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
+                    ls += s[r];
+                }
+                l_run += halves_sum(ls);
                 TR::pv(vreg, s, o, c, hf);
             } else if (MODE == 1) {
                 const float m_new = vmax(m_run, tile_max(s) * sc);
@@ -349,7 +350,7 @@ struct FaKernel {
 
         // ---------------- epilogue: O = O^T / l (wave ks == 0) ----------------
         if (ks == 0 && qi < Sq) {
-            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
@@ -375,7 +376,8 @@ template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
 __global__ __launch_bounds__(NQS* NKS * 64) void fa_fwd_kernel(AttnArgs a) {
     using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>;
     __shared__ __attribute__((aligned(16))) unsigned char lds[K::LDS_BYTES];
-    K::run(a, lds);
+    __shared__ int simd_slots[NQS * NKS];
+    K::run(a, lds, simd_slots);
 }
 
 template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>

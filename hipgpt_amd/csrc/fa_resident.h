@@ -14,7 +14,8 @@
 //     tile t before it waits on tile t, so the wait always ends; there is no
 //     workgroup barrier after the first, so waves with little causal work
 //     finish early instead of idling in lockstep.
-//   * Balance: wave w runs on SIMD w % 4.  The waves of SIMD s take query
+//   * Balance: the waves are ranked by the SIMD the hardware placed them on
+//     (simd_rank).  With NW/4 waves per SIMD, the waves of SIMD s take query
 //     sub-blocks s and NQS-1-s (NQS = 8), and with NKS = 2 each sub-block's
 //     tiles alternate between two waves, so every SIMD carries the same
 //     causal work; the NKS partial (m, l, O) are merged in LDS at the end.
@@ -55,13 +56,14 @@ struct FaResident {
     static constexpr int HEAD_BYTES = 256 + ML_BYTES;
     static constexpr int MERGE_BYTES = NKS > 1 ? NW * 64 * 16 * NDB * 4 : 0;
 
-    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max) {
+    __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max,
+                                               int* simd_slots) {
         E* const tiles = reinterpret_cast<E*>(lds_raw + HEAD_BYTES);
         int* const cnt = reinterpret_cast<int*>(lds_raw);  // 64 arrival counters
 
         const int tid = threadIdx.x;
         const int lane = tid & 63;
-        const int wave = tid >> 6;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31;
         const int hf = lane >> 5;
 
@@ -71,9 +73,11 @@ struct FaResident {
         const int qb = CAUSAL ? a.n_qblk - 1 - rank : rank;
         const int b = bh / a.H;
         const int h = bh % a.H;
-        // Waves s, s+4, s+8, s+12 share SIMD s: sub-blocks s and NQS-1-s, key
-        // splits 0 and 1.
-        const int simd = wave & 3, grp = wave >> 2;
+        // Ranked by SIMD, waves 4j .. 4j+3 of the ranking sit on SIMD j when the
+        // hardware puts NW/4 waves on each SIMD: the waves of a SIMD take
+        // sub-blocks s and NQS-1-s, key splits 0 and 1.
+        const int rk = simd_rank<NW>(simd_slots, wave, lane);
+        const int simd = rk / (NW / 4), grp = rk % (NW / 4);
         const int sub = (grp & 1) ? NQS - 1 - simd : simd;
         const int ks = grp >> 1;
         const int slot = sub * NKS + ks;
@@ -168,24 +172,26 @@ struct FaResident {
             floatx16 s = scores(t);
             typename TR::VReg vreg;
             TR::load_v(vreg, tiles + t * TILE_ELEMS + TR::KTILE, c, hf);
-            const float m_new = vmax(m_run, tile_max(s) * sc);
-            float ls = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] = fast_exp2(fmaf(s[r], sc, -m_new));
-                ls += s[r];
-            }
-            ls = halves_sum(ls);
-            if (__any(m_new != m_run)) {
+            // lazy rescale (kLazyMax): raise the running max only when a row's
+            // tile max exceeds it by more than the threshold
+            const float tmax = tile_max(s) * sc;
+            if (__any(tmax > m_run + kLazyMax)) {
+                const float m_new = vmax(m_run, tmax);
                 const float alpha = fast_exp2(m_run - m_new);
                 l_run *= alpha;
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                m_run = m_new;
             }
-            l_run += ls;
-            m_run = m_new;
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
+                ls += s[r];
+            }
+            l_run += halves_sum(ls);
             TR::pv(vreg, s, o, c, hf);
         };
         auto stats = [&](int t) {
@@ -328,7 +334,7 @@ struct FaResident {
         }
 
         if (ks == 0 && qi < Sq) {
-            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
@@ -344,7 +350,8 @@ struct FaResident {
 template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
 __global__ __launch_bounds__(NQS* NKS * 64) void fa_resident_kernel(AttnArgs a, int ntiles_max) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_dyn[];
-    FaResident<TR, NQS, NKS, L, CAUSAL, PROBS>::run(a, lds_dyn, ntiles_max);
+    __shared__ int simd_slots[NQS * NKS];
+    FaResident<TR, NQS, NKS, L, CAUSAL, PROBS>::run(a, lds_dyn, ntiles_max, simd_slots);
 }
 
 // Dynamic-LDS bytes for a resident launch over all ceil(Sk / 32) key tiles
