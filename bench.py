@@ -128,7 +128,7 @@ def make_call(cfg, torch, A, dev):
         bias = torch.randn(N, device=dev, generator=g)
         c = torch.empty(M, N, device=dev)
         return (lambda: P.launch_matmul_add_bias(a, w, bias, c, M, K, N),
-                {"entry": "launch_matmul_add_bias", "M": M, "N": N, "K": K})
+                {"entry": "launch_matmul_add_bias (null stream)", "M": M, "N": N, "K": K})
     if kind in ("sdp", "softmax", "wsum"):
         x = torch.randn(3, B * Sq, D, device=dev, generator=g)
         sc = torch.randn(B * Sq, Sk, device=dev, generator=g)
@@ -168,9 +168,20 @@ def make_call(cfg, torch, A, dev):
     return lambda: A.attention(q, k, v, out=out, probs=p, causal=causal), {"layout": "[B,S,H,D]"}
 
 
-def time_call(fn, steps, warmup, torch):
-    for _ in range(warmup):
+def time_call(fn, steps, warmup, torch, min_warm_s=0.2):
+    """ms per call over exactly `steps` back-to-back calls, HIP events on the
+    stream the calls launch on.  The untimed warm-up is `warmup` calls and at
+    least `min_warm_s` seconds of calls right before the timed region: the
+    MI355X needs ~0.1 s of load to reach its steady clock, and an idle gap
+    before the timed calls (allocation, another config's set-up) would
+    otherwise be timed at the lower clock."""
+    n = 0
+    t_end = time.perf_counter() + min_warm_s
+    while n < warmup or time.perf_counter() < t_end:
         fn()
+        n += 1
+        if n % 50 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()  # the stream the library launches on
     start = torch.cuda.Event(enable_timing=True)
@@ -183,7 +194,7 @@ def time_call(fn, steps, warmup, torch):
     return start.elapsed_time(stop) / steps  # ms per call
 
 
-def cpu_baseline(nthreads, min_seconds=2.0):
+def cpu_baseline(nthreads, min_seconds=10.0):
     """The oracle's scalar restatement of the reference kernel HipGPT runs for
     c1 (flash_attention_kernel<32>, causal-restricted) on the whole c1
     problem, on the host cores; repeated until min_seconds have elapsed,
@@ -315,7 +326,7 @@ def main():
     if not args.no_cpu:
         cpu1, dt1, n1 = cpu_baseline(1)
         ncores = min(16, os.cpu_count() or 1)
-        cpun, dtn, _ = cpu_baseline(ncores)
+        cpun, dtn, _ = cpu_baseline(ncores, min_seconds=2.0)
         line["cpu_baseline"] = {
             "value": round(cpu1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"whole c1 problem (causal, 256 (b,h) pairs) through the scalar restatement of "
