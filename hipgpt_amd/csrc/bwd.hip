@@ -7,8 +7,9 @@
 //   Dq_i = sum_j P_ij (dO_i . V_j)       (= dO_i . (P V)_i)
 //   dS   = P o (dO V^T - Dq)
 //   dQ = c dS K,   dK = c dS^T Q,   dV = P^T dO
-// Two kernels, every gradient element written exactly once (no atomics, no
-// memset):
+// Head dims 32 and 64 with 16-byte aligned rows run the LDS-tiled kernels of
+// bwd_tiled.h; the kernels below serve every other problem.  Two kernels,
+// every gradient element written exactly once (no atomics, no memset):
 //   * query-stationary (one wave per 32 queries): pass 1 forms (P V)_i on
 //     MFMA and Dq_i = dO_i . (P V)_i (stored to a B*H*S workspace); pass 2
 //     forms dP^T = V dO^T, dS, and dQ^T += K^T dS^T.
@@ -20,6 +21,7 @@
 // (b, h)) in the operand layouts; the fa_common.h accumulator layout applies.
 // Causal (extended API only) skips tiles of P that lie wholly above the
 // diagonal, where a causal forward wrote zeros.
+#include "bwd_tiled.h"
 #include "common.h"
 #include "fa_common.h"
 #include "kernels.h"
@@ -301,7 +303,36 @@ hipError_t launch_dp(const BwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
+// Workgroup shapes of the tiled kernels: query-stationary NQS x NKS,
+// key-stationary NKB x NQS.  4 x 1 for both was best or within 3% of the
+// best of nine shapes on MI355X for the c1 causal, c1 non-causal and c2
+// causal backward.
+#ifndef HIPGPT_BWDQ_NQS
+#define HIPGPT_BWDQ_NQS 4
+#endif
+#ifndef HIPGPT_BWDQ_NKS
+#define HIPGPT_BWDQ_NKS 1
+#endif
+#ifndef HIPGPT_BWDKV_NKB
+#define HIPGPT_BWDKV_NKB 4
+#endif
+#ifndef HIPGPT_BWDKV_NQS
+#define HIPGPT_BWDKV_NQS 1
+#endif
+
+bool bwd_tiled_ok(const BwdArgs& a) {
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    return (a.D == 32 || a.D == 64) && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) && al(a.k) &&
+           al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) && al(a.probs) &&
+           ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
+}
+
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
+    if (bwd_tiled_ok(a)) {
+        if (a.D == 32)
+            return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
+        return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
+    }
     if (a.D <= 32) return launch_dp<32>(a, s);
     if (a.D <= 64) return launch_dp<64>(a, s);
     if (a.D <= 128) return launch_dp<128>(a, s);

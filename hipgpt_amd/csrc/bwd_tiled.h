@@ -1,0 +1,500 @@
+// bwd_tiled.h -- LDS-tiled MFMA kernels of the attention backward on the
+// forward's probabilities (HipGPT src/hip_kernels.cpp:1159-1272), for head
+// dims 32 and 64 with 16-byte aligned rows.
+//
+// Math per (b, h), scale c = 1/sqrt(D):
+//   dP = dO V^T,  Dq_i = sum_j P_ij dP_ij,  dS = P o (dP - Dq),
+//   dQ = c dS K,  dK = c dS^T Q,  dV = P^T dO.
+// Two kernels, every gradient element written once (no atomics, no memset):
+//   * bwd_q_kernel (query-stationary): wave (qs, ks) owns 32 queries and every
+//     NKS-th key tile.  One pass over the keys accumulates
+//       A = (P o dP) K,  Bm = P K,  Dq = rowsum(P o dP),
+//     and dQ = c (A - Dq Bm), so P and V are read once; the key splits are
+//     summed through LDS.  Dq goes to the workspace for the second kernel.
+//   * bwd_kv_kernel (key-stationary): wave (ks, qs) owns 32 keys (V in
+//     registers) and every NQS-th query tile; dP = dO V^T lands with one key
+//     per lane and the queries in the accumulator's register order, which is
+//     the B-operand layout of dV^T += dO^T P and dK^T += Q^T dS, so P and dS
+//     never leave registers; the query splits are summed through LDS.
+// Operand tiles go global -> registers -> LDS, double buffered, one barrier
+// per stage (one key tile, resp. NQS query tiles), with the next stage's
+// loads in flight during the MFMAs.  LDS tiles are row-major (pitch DP+4:
+// conflict-free ds_read_b128 along the head dim) or transposed (pitch 36:
+// ds_read_b128 along the 32 rows).  P is read straight from global memory in
+// the layout each kernel needs: rows of 16 bytes (query-stationary) or
+// 128-byte row segments per half-wave (key-stationary).
+// Causal (probs zero above the diagonal) skips key tiles past a query
+// tile's diagonal (query-stationary) and query tiles before a key tile's
+// diagonal (key-stationary).
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "fa_common.h"
+#include "kernels.h"
+
+namespace hipgpt {
+namespace bwd {
+
+using fa::acc_key;
+using fa::BK;
+using fa::halves_sum;
+
+constexpr int TP = BK + 4;  // pitch of a transposed tile (rows are head dims)
+
+template <int DP>
+struct Tiles {
+    static constexpr int RP = DP + 4;           // pitch of a row-major tile
+    static constexpr int ROW = BK * RP;         // floats of a row-major tile
+    static constexpr int TR = DP * TP;          // floats of a transposed tile
+    static constexpr int CPR = DP / 4;          // 16-byte chunks per row
+    static constexpr int CPT = BK * CPR;        // chunks per tile
+
+    __device__ __forceinline__ static void store_row(float* t, int r, int cc, const floatx4& v) {
+        *reinterpret_cast<floatx4*>(t + r * RP + cc * 4) = v;
+    }
+    __device__ __forceinline__ static void store_tr(float* t, int r, int cc, const floatx4& v) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[(cc * 4 + j) * TP + r] = v[j];
+    }
+    // Chain over the head dim: D[m = row c of `rt`][n = c] += sum_d rt[c][d] b[d],
+    // lane (c, h) taking d = h*DP/2 + s (b holds the lane's DP/2 values).
+    __device__ __forceinline__ static void dchain(floatx16& acc, const float* rt, const float* b, int c, int hf) {
+        const float* rr = rt + c * RP + hf * (DP / 2);
+#pragma unroll
+        for (int j = 0; j < DP / 8; ++j) {
+            const floatx4 kv = *reinterpret_cast<const floatx4*>(rr + 4 * j);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[u], b[4 * j + u], acc, 0, 0, 0);
+        }
+    }
+    // Chain over the 32 tile rows: acc[n][db][m = d][n = c] += sum_k tt[d][k] x[n][k][c]
+    // for N right-hand operands sharing the A tile, x in accumulator register
+    // order (register t <-> row acc_key(t, h)).
+    template <int N>
+    __device__ __forceinline__ static void rchain(floatx16 (*acc)[DP / 32], const float* tt, const floatx16* x, int c,
+                                                  int hf) {
+#pragma unroll
+        for (int db = 0; db < DP / 32; ++db) {
+            const float* p = tt + (db * 32 + c) * TP + 4 * hf;
+            floatx4 blk[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) blk[g] = *reinterpret_cast<const floatx4*>(p + 8 * g);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int n = 0; n < N; ++n)
+                        acc[n][db] = __builtin_amdgcn_mfma_f32_32x32x2f32(blk[g][u], x[n][4 * g + u], acc[n][db], 0, 0, 0);
+        }
+    }
+};
+
+// 16-byte chunks of `rows` consecutive rows (row stride ts floats) through a
+// buffer resource whose range ends at the slice's last row: rows past it read
+// as zero.
+struct RowLoader {
+    __amdgpu_buffer_rsrc_t rs;
+    int row_bytes;
+    __device__ __forceinline__ void init(const float* base, int64_t ts, int S, int D) {
+        rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)(((int64_t)(S - 1) * ts + D) * 4),
+                                               kBufferFlags);
+        row_bytes = (int)(ts * 4);
+    }
+    __device__ __forceinline__ floatx4 load(int row, int col4) const {
+        return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, row * row_bytes + col4 * 16, 0, 0));
+    }
+};
+
+// ----------------------------------------------------------------- dQ, Dq
+template <int DP, int NQS, int NKS, bool CAUSAL>
+struct BwdQ {
+    using T = Tiles<DP>;
+    static constexpr int NW = NQS * NKS;
+    static constexpr int NT = NW * 64;
+    static constexpr int NDB = DP / 32;
+    // stage: NKS key tiles, each V row-major + K transposed
+    static constexpr int STAGE = NKS * (T::ROW + T::TR);
+    static constexpr int PER = (2 * NKS * T::CPT + NT - 1) / NT;  // chunks per thread per stage
+    static constexpr int MERGE = NW * 64 * (2 * 16 * NDB + 1);
+    static constexpr int LDS_FLOATS = 2 * STAGE > MERGE ? 2 * STAGE : MERGE;
+
+    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nqb) {
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int c = lane & 31, hf = lane >> 5;
+        const int BH = a.B * a.H;
+        const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
+        const int qb = CAUSAL ? nqb - 1 - rank : rank;
+        const int role = (fa::simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
+        const int qs = role / NKS, ks = role % NKS;
+        const int b = bh / a.H, h = bh % a.H;
+        const int S = a.S;
+        const int q0 = qb * NQS * BK, qw0 = q0 + qs * BK, qi = qw0 + c;
+        const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
+        const int kend = CAUSAL ? min(S, q0 + NQS * BK) : S;
+        const int ntiles = (kend + BK - 1) / BK;
+        const int wtiles = qw0 < S ? (CAUSAL ? (min(S, qw0 + BK) + BK - 1) / BK : ntiles) : 0;
+        const int nstages = (ntiles + NKS - 1) / NKS;
+
+        // dO (B operand of dP^T = V dO^T): lane (c, h) holds dO[qi][h*DP/2 + s]
+        float go[DP / 2];
+        {
+            const float* g = a.go + base + (int64_t)qi * a.ts + hf * (DP / 2);
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const floatx4 t = qi < S ? *reinterpret_cast<const floatx4*>(g + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) go[s + j] = t[j];
+            }
+        }
+        RowLoader kl, vl;
+        kl.init(a.k + base, a.ts, S, a.D);
+        vl.init(a.v + base, a.ts, S, a.D);
+        floatx4 stg[PER];
+        auto load = [&](int st) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if ((2 * NKS * T::CPT) % NT != 0 && f >= 2 * NKS * T::CPT) break;
+                const int isk = f >= NKS * T::CPT;
+                const int g = isk ? f - NKS * T::CPT : f;
+                const int row = st * NKS * BK + g / T::CPR;
+                stg[i] = isk ? kl.load(row, g % T::CPR) : vl.load(row, g % T::CPR);
+            }
+        };
+        auto store = [&](float* dst) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if ((2 * NKS * T::CPT) % NT != 0 && f >= 2 * NKS * T::CPT) break;
+                const int isk = f >= NKS * T::CPT;
+                const int g = isk ? f - NKS * T::CPT : f;
+                const int kt = g / T::CPT, r = (g % T::CPT) / T::CPR, cc = g % T::CPR;
+                float* tile = dst + kt * (T::ROW + T::TR);
+                if (isk)
+                    T::store_tr(tile + T::ROW, r, cc, stg[i]);
+                else
+                    T::store_row(tile, r, cc, stg[i]);
+            }
+        };
+
+        floatx16 acc[2][NDB];  // [0] = A^T, [1] = Bm^T, both [d][query]
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
+        float ld = 0.f;
+        const float* prow = a.probs + ((int64_t)bh * S + qi) * S;
+        const bool pvec = (S & 3) == 0;
+
+        auto compute = [&](int st, const float* cur) {
+            const int t = st * NKS + ks;
+            if (t >= wtiles) return;
+            const float* tile = cur + ks * (T::ROW + T::TR);
+            // P in accumulator order: register r <-> key t*32 + acc_key(r, h)
+            floatx16 x[2];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int k0 = t * BK + 8 * g + 4 * hf;
+                floatx4 pv;
+                if (pvec && qi < S && k0 + 3 < S) {
+                    pv = *reinterpret_cast<const floatx4*>(prow + k0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pv[j] = (qi < S && k0 + j < S) ? prow[k0 + j] : 0.f;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[1][4 * g + j] = pv[j];
+            }
+            floatx16 dp;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] = 0.f;
+            T::dchain(dp, tile, go, c, hf);  // dP^T, register r <-> key acc_key(r, h)
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                x[0][r] = x[1][r] * dp[r];
+                s += x[0][r];
+            }
+            ld += s;
+            T::template rchain<2>(acc, tile + T::ROW, x, c, hf);  // A^T += K^T (P o dP)^T, Bm^T += K^T P^T
+        };
+
+        if (nstages > 0) {
+            load(0);
+            store(lds);
+        }
+        __syncthreads();
+        for (int st = 0; st < nstages; ++st) {
+            if (st + 1 < nstages) load(st + 1);
+            compute(st, lds + (st & 1) * STAGE);
+            if (st + 1 < nstages) store(lds + ((st + 1) & 1) * STAGE);
+            __syncthreads();
+        }
+
+        // sum the key splits (wave ks == 0 keeps the sub-block)
+        if (NKS > 1) {
+            float* const mo = lds;  // [NW][2*16*NDB + 1][64]
+            constexpr int W = 2 * 16 * NDB + 1;
+            if (ks != 0) {
+#pragma unroll
+                for (int n = 0; n < 2; ++n)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) mo[(role * W + (n * NDB + db) * 16 + r) * 64 + lane] = acc[n][db][r];
+                mo[(role * W + W - 1) * 64 + lane] = ld;
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int j = 1; j < NKS; ++j) {
+#pragma unroll
+                    for (int n = 0; n < 2; ++n)
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[n][db][r] += mo[((role + j) * W + (n * NDB + db) * 16 + r) * 64 + lane];
+                    ld += mo[((role + j) * W + W - 1) * 64 + lane];
+                }
+            }
+        }
+        if (ks == 0 && qi < S) {
+            const float dq = halves_sum(ld);
+            if (hf == 0) a.dvec[(int64_t)bh * S + qi] = dq;
+            float* out = a.dq + base + (int64_t)qi * a.ts;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    floatx4 v;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        v[j] = a.scale * fmaf(-dq, acc[1][db][4 * g + j], acc[0][db][4 * g + j]);
+                    *reinterpret_cast<floatx4*>(out + db * 32 + 8 * g + 4 * hf) = v;
+                }
+        }
+    }
+};
+
+// ----------------------------------------------------------------- dK, dV
+template <int DP, int NKB, int NQS, bool CAUSAL>
+struct BwdKV {
+    using T = Tiles<DP>;
+    static constexpr int NW = NKB * NQS;
+    static constexpr int NT = NW * 64;
+    static constexpr int NDB = DP / 32;
+    // stage: NQS query tiles, each dO row-major + dO transposed + Q transposed + Dq
+    static constexpr int QT = T::ROW + 2 * T::TR + BK;
+    static constexpr int STAGE = NQS * QT;
+    static constexpr int PER = (2 * NQS * T::CPT + NT - 1) / NT;
+    static constexpr int MERGE = NW * 64 * (2 * 16 * NDB);
+    static constexpr int LDS_FLOATS = 2 * STAGE > MERGE ? 2 * STAGE : MERGE;
+
+    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nkb) {
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int c = lane & 31, hf = lane >> 5;
+        const int BH = a.B * a.H;
+        const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
+        const int kb = rank;  // key block; causal: block 0 sees the most query tiles and launches first
+        const int role = (fa::simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
+        const int ksub = role / NQS, qsp = role % NQS;
+        const int b = bh / a.H, h = bh % a.H;
+        const int S = a.S;
+        const int k0 = kb * NKB * BK, kw0 = k0 + ksub * BK, kj = kw0 + c;
+        const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
+        const int nq = (S + BK - 1) / BK;
+        // query tiles [it0, nq): causal starts at the workgroup's first key tile
+        const int it0 = CAUSAL ? k0 / BK : 0;
+        const int wit0 = CAUSAL ? kw0 / BK : 0;  // this wave's first useful query tile
+        const int nstages = (nq - it0 + NQS - 1) / NQS;
+
+        // V (B operand of dP = dO V^T): lane (c, h) holds V[kj][h*DP/2 + s]
+        float vr[DP / 2];
+        {
+            const float* vp = a.v + base + (int64_t)kj * a.ts + hf * (DP / 2);
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const floatx4 t = kj < S ? *reinterpret_cast<const floatx4*>(vp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vr[s + j] = t[j];
+            }
+        }
+        RowLoader gl, ql;
+        gl.init(a.go + base, a.ts, S, a.D);
+        ql.init(a.q + base, a.ts, S, a.D);
+        floatx4 stg[PER];
+        float dqs = 0.f;  // Dq value this thread stages
+        auto load = [&](int st) {
+            const int qt0 = it0 + st * NQS;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if ((2 * NQS * T::CPT) % NT != 0 && f >= 2 * NQS * T::CPT) break;
+                const int isq = f >= NQS * T::CPT;
+                const int g = isq ? f - NQS * T::CPT : f;
+                const int row = qt0 * BK + g / T::CPR;
+                stg[i] = isq ? ql.load(row, g % T::CPR) : gl.load(row, g % T::CPR);
+            }
+            if (tid < NQS * BK) {
+                const int qrow = qt0 * BK + tid;
+                dqs = qrow < S ? a.dvec[(int64_t)bh * S + qrow] : 0.f;
+            }
+        };
+        auto store = [&](float* dst) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int f = tid + i * NT;
+                if ((2 * NQS * T::CPT) % NT != 0 && f >= 2 * NQS * T::CPT) break;
+                const int isq = f >= NQS * T::CPT;
+                const int g = isq ? f - NQS * T::CPT : f;
+                const int qt = g / T::CPT, r = (g % T::CPT) / T::CPR, cc = g % T::CPR;
+                float* tile = dst + qt * QT;
+                if (isq) {
+                    T::store_tr(tile + T::ROW + T::TR, r, cc, stg[i]);
+                } else {
+                    T::store_row(tile, r, cc, stg[i]);
+                    T::store_tr(tile + T::ROW, r, cc, stg[i]);
+                }
+            }
+            if (tid < NQS * BK) dst[(tid / BK) * QT + T::ROW + 2 * T::TR + tid % BK] = dqs;
+        };
+
+        floatx16 acc[2][NDB];  // [0] = dV^T, [1] = dK^T (unscaled), both [d][key]
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
+        const float* pcol = a.probs + (int64_t)bh * S * S + kj;
+
+        auto compute = [&](int st, const float* cur) {
+            const int it = it0 + st * NQS + qsp;
+            if (it >= nq || it < wit0) return;
+            const float* tile = cur + qsp * QT;
+            floatx16 x[2];  // [0] = P, [1] = dS, register r <-> query it*32 + acc_key(r, h)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int qr = it * BK + acc_key(r, hf);
+                x[0][r] = (qr < S && kj < S) ? pcol[(int64_t)qr * S] : 0.f;
+            }
+            floatx16 dp;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] = 0.f;
+            T::dchain(dp, tile, vr, c, hf);  // dP, register r <-> query acc_key(r, h)
+            const float* dqt = tile + T::ROW + 2 * T::TR;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const floatx4 dq = *reinterpret_cast<const floatx4*>(dqt + 8 * g + 4 * hf);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) x[1][4 * g + j] = x[0][4 * g + j] * (dp[4 * g + j] - dq[j]);
+            }
+            // dV^T += dO^T P, dK^T += Q^T dS: two A tiles, one per product
+            T::template rchain<1>(&acc[0], tile + T::ROW, &x[0], c, hf);
+            T::template rchain<1>(&acc[1], tile + T::ROW + T::TR, &x[1], c, hf);
+        };
+
+        if (nstages > 0) {
+            load(0);
+            store(lds);
+        }
+        __syncthreads();
+        for (int st = 0; st < nstages; ++st) {
+            if (st + 1 < nstages) load(st + 1);
+            compute(st, lds + (st & 1) * STAGE);
+            if (st + 1 < nstages) store(lds + ((st + 1) & 1) * STAGE);
+            __syncthreads();
+        }
+
+        if (NQS > 1) {
+            float* const mo = lds;  // [NW][2*16*NDB][64]
+            constexpr int W = 2 * 16 * NDB;
+            if (qsp != 0) {
+#pragma unroll
+                for (int n = 0; n < 2; ++n)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) mo[(role * W + (n * NDB + db) * 16 + r) * 64 + lane] = acc[n][db][r];
+            }
+            __syncthreads();
+            if (qsp == 0) {
+#pragma unroll
+                for (int j = 1; j < NQS; ++j)
+#pragma unroll
+                    for (int n = 0; n < 2; ++n)
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[n][db][r] += mo[((role + j) * W + (n * NDB + db) * 16 + r) * 64 + lane];
+            }
+        }
+        if (qsp == 0 && kj < S) {
+            float* dvp = a.dv + base + (int64_t)kj * a.ts;
+            float* dkp = a.dk + base + (int64_t)kj * a.ts;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d0 = db * 32 + 8 * g + 4 * hf;
+                    *reinterpret_cast<floatx4*>(dvp + d0) =
+                        floatx4{acc[0][db][4 * g], acc[0][db][4 * g + 1], acc[0][db][4 * g + 2], acc[0][db][4 * g + 3]};
+                    *reinterpret_cast<floatx4*>(dkp + d0) =
+                        floatx4{a.scale * acc[1][db][4 * g], a.scale * acc[1][db][4 * g + 1],
+                                a.scale * acc[1][db][4 * g + 2], a.scale * acc[1][db][4 * g + 3]};
+                }
+        }
+    }
+};
+
+template <int DP, int NQS, int NKS, bool CAUSAL>
+__global__ __launch_bounds__(NQS* NKS * 64) void bwd_q_kernel(BwdArgs a, int nqb) {
+    using K = BwdQ<DP, NQS, NKS, CAUSAL>;
+    __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
+    __shared__ int simd_slots[NQS * NKS];
+    K::run(a, lds, simd_slots, nqb);
+}
+
+template <int DP, int NKB, int NQS, bool CAUSAL>
+__global__ __launch_bounds__(NKB* NQS * 64) void bwd_kv_kernel(BwdArgs a, int nkb) {
+    using K = BwdKV<DP, NKB, NQS, CAUSAL>;
+    __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
+    __shared__ int simd_slots[NKB * NQS];
+    K::run(a, lds, simd_slots, nkb);
+}
+
+// Both kernels for one problem (the second reads the first's Dq).
+template <int DP, int QNQS, int QNKS, int KNKB, int KNQS>
+hipError_t launch_tiled(const BwdArgs& a, hipStream_t s) {
+    const int BH = a.B * a.H;
+    const int nqb = (a.S + QNQS * BK - 1) / (QNQS * BK);
+    const int nkb = (a.S + KNKB * BK - 1) / (KNKB * BK);
+    const int64_t g1 = (int64_t)nqb * BH, g2 = (int64_t)nkb * BH;
+    if (g1 <= 0 || g1 > 0x7fffffff || g2 > 0x7fffffff) return hipErrorInvalidConfiguration;
+    if (a.causal)
+        hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, true>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s, a, nqb);
+    else
+        hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, false>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s, a,
+                           nqb);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (a.causal)
+        hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, true>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0, s, a,
+                           nkb);
+    else
+        hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, false>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0, s, a,
+                           nkb);
+    return hipGetLastError();
+}
+
+}  // namespace bwd
+}  // namespace hipgpt
