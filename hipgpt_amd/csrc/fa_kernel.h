@@ -29,6 +29,12 @@
 namespace hipgpt {
 namespace fa {
 
+// Start stagger of short causal grids (see FaKernel::run): 20 ticks of the
+// 100 MHz s_memrealtime counter = 200 ns per launch rank, for grids of at
+// most 4 query blocks per (batch, head).
+constexpr unsigned long long kStaggerTicks = 20;
+constexpr int kStaggerMaxBlocks = 4;
+
 template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
 struct FaKernel {
     static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");
@@ -160,6 +166,16 @@ struct FaKernel {
         const E* Kp = static_cast<const E*>(a.k) + b * a.k_bs + h * a.k_hs;
         const E* Vp = static_cast<const E*>(a.v) + b * a.v_bs + h * a.v_hs;
 
+        // Short causal problems (a few query blocks per (batch, head), the
+        // whole grid resident at once) start with every workgroup loading its
+        // first stage at the same moment, and the first tile computes only
+        // when that burst has drained.  Launch rank r waits r * 200 ns first,
+        // so the longest query blocks (rank 0) get their operands earliest
+        // and compute while the shorter ones load (c1: 16.4 -> 15.9 us).
+        if (CAUSAL && a.n_qblk <= kStaggerMaxBlocks && rank > 0) {
+            const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)rank * kStaggerTicks;
+            for (int i = 0; i < 1024 && __builtin_amdgcn_s_memrealtime() < t_end; ++i) __builtin_amdgcn_s_sleep(2);
+        }
         const TileRange tr = tile_range<CAUSAL>(q0, qw0, NQS * QW, Sq, Sk, off);
         const int nstages = (tr.ntiles + NKS - 1) / NKS;
         const int wtiles = tr.wtiles;
