@@ -120,8 +120,11 @@ struct B16Traits {
     }
 };
 
+// Workgroup shape: 4 query sub-blocks share each K/V stage (bf16 tiles are
+// short on the matrix cores, so the stage's loads, LDS stores and barrier
+// are amortised over more work); 4 x 2 measured best of 2x2, 4x1, 4x2, 2x4, 8x1.
 #ifndef HIPGPT_BF16_NQS
-#define HIPGPT_BF16_NQS 2
+#define HIPGPT_BF16_NQS 4
 #endif
 #ifndef HIPGPT_BF16_NKS
 #define HIPGPT_BF16_NKS 2
