@@ -62,7 +62,10 @@ def test_strerror_and_host_validation():
     assert L.hipgpt_attn_decode(p, p, p, p, 1, 1, 512, 64, *([0] * 10), -1.0, 4, None, 0, None) == _lib.ERR_WORKSPACE
     assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 4) == 2 * 3 * 4 * 66 * 4
     assert L.hipgpt_attn_decode_workspace_bytes(2, 3, 64, 1) == 0
-    assert L.hipgpt_attn_decode_default_splits(64, 12, 2048) >= 2
+    # one split once B*H alone fills the chip (c5), more for small batches
+    assert L.hipgpt_attn_decode_default_splits(64, 12, 2048) == 1
+    assert L.hipgpt_attn_decode_default_splits(1, 12, 32768) >= 16
+    assert L.hipgpt_attn_decode_default_splits(4, 12, 200) == 1  # no split below 128 keys
     assert L.hipgpt_attn_bwd_workspace_bytes(2, 8, 3) == 2 * 3 * 8 * 4
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 64, 2, 0, None, 0, None) == _lib.ERR_WORKSPACE
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 63, 2, 0, p, 1 << 20, None) == _lib.ERR_INVALID
