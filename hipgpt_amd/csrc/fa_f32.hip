@@ -145,7 +145,10 @@ struct F32Traits {
     }
 };
 
-// Workgroup shape per padded head dim: NQS query sub-blocks x NKS key splits.
+// Workgroup shape per padded head dim: NQS query sub-blocks x NKS key splits,
+// measured on MI355X with waves ranked by SIMD: D=32 2x2 (c1), D=64 4x2 (c3),
+// D=128 8x1 (c4) -- the larger head dims run 2 waves per SIMD, and more query
+// sub-blocks per workgroup share each K/V stage.
 #ifndef HIPGPT_F32_D32_NQS
 #define HIPGPT_F32_D32_NQS 2
 #endif
@@ -153,13 +156,13 @@ struct F32Traits {
 #define HIPGPT_F32_D32_NKS 2
 #endif
 #ifndef HIPGPT_F32_D64_NQS
-#define HIPGPT_F32_D64_NQS 2
+#define HIPGPT_F32_D64_NQS 4
 #endif
 #ifndef HIPGPT_F32_D64_NKS
 #define HIPGPT_F32_D64_NKS 2
 #endif
 #ifndef HIPGPT_F32_D128_NQS
-#define HIPGPT_F32_D128_NQS 4
+#define HIPGPT_F32_D128_NQS 8
 #endif
 #ifndef HIPGPT_F32_D128_NKS
 #define HIPGPT_F32_D128_NKS 1
