@@ -62,4 +62,15 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin (id % 8), and each XCD
+// has its own L2.  xcd_remap renumbers a 1-D grid so that XCD x runs the
+// contiguous logical range [x*per, (x+1)*per), per = total / 8 (ids past
+// 8*per keep their number): neighbouring logical workgroups, which share
+// operands, then share one L2.  A bijection on [0, total).
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+    const int per = total / 8;
+    if (id >= 8 * per) return id;
+    return (id % 8) * per + id / 8;
+}
+
 }  // namespace hipgpt

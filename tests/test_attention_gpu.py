@@ -268,8 +268,15 @@ def test_bf16_baseline_config_c3(dev, causal):
 
 
 # ---------------------------------------------------------------- unfused helpers
+# Row kernels (D = 32/64/128, aligned): S on and off the 32-row tile grid, the
+# register-resident softmax at 256/512/1024/2048 columns and the sweep softmax
+# beyond; keys split over workgroups (few sequences) and the grouped weighted
+# sum (>= 256 query groups, spare waves when S/32 is not a multiple of 4);
+# per-element kernels: other D, S % 4 != 0 (weighted sum).
 @pytest.mark.parametrize("B,S,D", [(1, 1, 8), (2, 33, 32), (1, 70, 48), (3, 64, 64), (2, 45, 128),
-                                   (1, 20, 160), (32, 256, 32)])
+                                   (1, 20, 160), (32, 256, 32), (2, 100, 64), (1, 36, 128), (1, 30, 32),
+                                   (2, 500, 32), (1, 1024, 64), (1, 2048, 128), (1, 2052, 32),
+                                   (256, 64, 32), (256, 70, 64), (256, 36, 128)])
 def test_unfused_helpers_match_oracle_and_reference(dev, B, S, D):
     """launch_scaled_dot_product / launch_softmax / launch_attention_weighted_sum
     (include/hip_kernels.h:44-46) against the oracle and, where the reference
@@ -299,3 +306,27 @@ def test_unfused_helpers_match_oracle_and_reference(dev, B, S, D):
         assert np.abs(host(scores) - host(rs)).max() <= 1e-4
         assert np.abs(host(probs) - host(rp)).max() <= TOL_P
         assert np.abs(host(out) - host(ro)).max() <= TOL_O
+
+
+def test_unfused_helpers_unaligned_views(dev):
+    """Buffers one float off 16-byte alignment take the per-element / sweep
+    kernels; results match the oracle as on aligned buffers."""
+    B, S, D = 2, 64, 32
+    x = O.fill_normal(4242, 3 * B * S * D).reshape(3, B * S, D)
+    flat = [torch.zeros(B * S * D + 1, device=dev) for _ in range(3)]
+    for t, a in zip(flat, x):
+        t[1:] = torch.from_numpy(a.reshape(-1)).to(dev)
+    dq, dk, dv = (t[1:] for t in flat)
+    sbuf = torch.full((B * S * S + 1,), float("nan"), device=dev)
+    pbuf = torch.full((B * S * S + 1,), float("nan"), device=dev)
+    obuf = torch.full((B * S * D + 1,), float("nan"), device=dev)
+    scores, probs, out = sbuf[1:], pbuf[1:], obuf[1:]
+    A.launch_scaled_dot_product(dq, dk, scores, B, S, D)
+    A.launch_softmax(scores, probs, B, S)
+    A.launch_attention_weighted_sum(probs, dv, out, B, S, D)
+    ws = O.scaled_dot_product(x[0], x[1], B, S, D)
+    assert np.abs(host(scores).reshape(B * S, S) - ws).max() <= 1e-4
+    wp = O.softmax_rows(host(scores).reshape(B * S, S), B, S)
+    assert np.abs(host(probs).reshape(B * S, S) - wp).max() <= TOL_P
+    wo = O.attention_weighted_sum(host(probs).reshape(B * S, S), x[2], B, S, D)
+    assert np.abs(host(out).reshape(B * S, D) - wo).max() <= TOL_O
