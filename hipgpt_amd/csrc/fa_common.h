@@ -111,6 +111,9 @@ __device__ __forceinline__ void store_probs_tile(float* prow, const floatx16& p,
     for (int g = 0; g < 4; ++g) {
         const int k0 = tb + 8 * g + 4 * hf;
         if (pvec && k0 + 3 < Sk) {
+            // Plain (not non-temporal) stores: each row gets 32 bytes per
+            // instruction, and L2 merges them into full lines (non-temporal
+            // partial-line stores measured 2x slower).
             *reinterpret_cast<floatx4*>(prow + k0) = floatx4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
         } else {
 #pragma unroll

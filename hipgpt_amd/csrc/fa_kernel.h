@@ -98,7 +98,7 @@ struct FaKernel {
             }
         }
 
-        template <int SL>
+        template <int SL, bool WV = true>
         __device__ __forceinline__ void load(int stage, int tid) {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -106,7 +106,8 @@ struct FaKernel {
                 if (VEC) {
                     if (CPS % NT == 0 || f < CPS) {
                         kr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
-                        vr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
+                        if (WV)
+                            vr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
                     }
                 } else {
                     const int row = f / CPR;  // 0 .. NKS*BK-1
@@ -114,11 +115,11 @@ struct FaKernel {
                     const int key = stage * NKS * BK + row;
                     const bool ok = (CPS % NT == 0 || f < CPS) && key < Sk;
                     kr[SL][i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
-                    vr[SL][i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
+                    if (WV) vr[SL][i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
                 }
             }
         }
-        template <int SL>
+        template <int SL, bool WV = true>
         __device__ __forceinline__ void store(E* stage, int tid) const {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -131,7 +132,7 @@ struct FaKernel {
                 E* Kt = stage + kt * TR::KTILE;
                 E* Vt = stage + NKS * TR::KTILE + kt * TR::VTILE;
                 TR::store_k_chunk(Kt, r, cc, kr[SL][i]);
-                TR::store_vt_chunk(Vt, r, cc, vr[SL][i]);
+                if (WV) TR::store_vt_chunk(Vt, r, cc, vr[SL][i]);
             }
         }
     };
@@ -259,18 +260,19 @@ struct FaKernel {
         // stage earlier) is written to LDS afterwards, so every global load
         // has two stages of compute to land.
         auto sweep = [&](auto mode_tag, float linv, float* prow, bool pvec) {
+            constexpr bool WV = decltype(mode_tag)::value != 1;  // the max/sum sweep stages no V
             if (nstages > 0) {
-                st.template load<0>(0, tid);
-                if (PF == 2 && nstages > 1) st.template load<PF - 1>(1, tid);
-                st.template store<0>(lds, tid);
+                st.template load<0, WV>(0, tid);
+                if (PF == 2 && nstages > 1) st.template load<PF - 1, WV>(1, tid);
+                st.template store<0, WV>(lds, tid);
             }
             __syncthreads();
             auto iter = [&](int i, auto slot_tag) {
                 constexpr int SL = decltype(slot_tag)::value;  // slot free for new loads
                 constexpr int NX = PF == 2 ? 1 - SL : 0;      // slot holding stage i+1
-                if (i + PF < nstages) st.template load<SL>(i + PF, tid);
+                if (i + PF < nstages) st.template load<SL, WV>(i + PF, tid);
                 compute(mode_tag, i, linv, prow, pvec);
-                if (i + 1 < nstages) st.template store<NX>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                if (i + 1 < nstages) st.template store<NX, WV>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
                 __syncthreads();
             };
             for (int i = 0; i < nstages; i += PF) {
