@@ -108,6 +108,18 @@ struct RowLoader {
     }
 };
 
+// Wave role from its SIMD rank sr and the workgroup's launch rank.  The
+// launch ranks of one (b, h) are dealt to the same CUs in turn, so a CU holds
+// one workgroup of each rank.  Rotating the roles by the rank spreads causal
+// work when there are as many ranks as roles; with two ranks (the c1 / c2
+// shapes: 4 roles of 5..8 and 1..4 tiles, resp. 8..5 and 4..1) the second rank
+// takes the roles in reverse SIMD order, so every SIMD carries 9 tiles instead
+// of 7..11.
+__device__ __forceinline__ int role_of(int sr, int rank, int nranks, int nw, bool causal) {
+    if (causal && nranks == 2) return rank ? nw - 1 - sr : sr;
+    return (sr + rank) % nw;
+}
+
 // ----------------------------------------------------------------- dQ, Dq
 template <int DP, int NQS, int NKS, bool CAUSAL>
 struct BwdQ {
@@ -128,7 +140,7 @@ struct BwdQ {
         const int BH = a.B * a.H;
         const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
         const int qb = CAUSAL ? nqb - 1 - rank : rank;
-        const int role = (fa::simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
+        const int role = role_of(fa::simd_rank<NW>(simd_slots, wave, lane), rank, nqb, NW, CAUSAL);
         const int qs = role / NKS, ks = role % NKS;
         const int b = bh / a.H, h = bh % a.H;
         const int S = a.S;
@@ -192,25 +204,34 @@ struct BwdQ {
         const float* prow = a.probs + ((int64_t)bh * S + qi) * S;
         const bool pvec = (S & 3) == 0;
 
+        // P of key tile t in accumulator order: piece g holds keys
+        // t*32 + 8g + 4h .. +3 (register 4g + j <-> key t*32 + acc_key(4g + j, h)).
+        auto load_p = [&](floatx4 (&pv)[4], int t) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int k0 = t * BK + 8 * g + 4 * hf;
+                if (pvec && qi < S && k0 + 3 < S) {
+                    pv[g] = *reinterpret_cast<const floatx4*>(prow + k0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pv[g][j] = (qi < S && k0 + j < S) ? prow[k0 + j] : 0.f;
+                }
+            }
+        };
+        // The next tile's P is requested while this tile's MFMAs run.
+        floatx4 pnext[4];
+        if (ks < wtiles) load_p(pnext, ks);
+
         auto compute = [&](int st, const float* cur) {
             const int t = st * NKS + ks;
             if (t >= wtiles) return;
             const float* tile = cur + ks * (T::ROW + T::TR);
-            // P in accumulator order: register r <-> key t*32 + acc_key(r, h)
             floatx16 x[2];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int k0 = t * BK + 8 * g + 4 * hf;
-                floatx4 pv;
-                if (pvec && qi < S && k0 + 3 < S) {
-                    pv = *reinterpret_cast<const floatx4*>(prow + k0);
-                } else {
+            for (int g = 0; g < 4; ++g)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) pv[j] = (qi < S && k0 + j < S) ? prow[k0 + j] : 0.f;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) x[1][4 * g + j] = pv[j];
-            }
+                for (int j = 0; j < 4; ++j) x[1][4 * g + j] = pnext[g][j];
+            if (t + NKS < wtiles) load_p(pnext, t + NKS);
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
@@ -304,7 +325,7 @@ struct BwdKV {
         const int BH = a.B * a.H;
         const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
         const int kb = rank;  // key block; causal: block 0 sees the most query tiles and launches first
-        const int role = (fa::simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
+        const int role = role_of(fa::simd_rank<NW>(simd_slots, wave, lane), rank, nkb, NW, CAUSAL);
         const int ksub = role / NQS, qsp = role % NQS;
         const int b = bh / a.H, h = bh % a.H;
         const int S = a.S;
@@ -376,16 +397,30 @@ struct BwdKV {
                 for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
         const float* pcol = a.probs + (int64_t)bh * S * S + kj;
 
+        // P column of query tile it, register r <-> query it*32 + acc_key(r, h)
+        auto load_p = [&](floatx16& pv, int it) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int qr = it * BK + acc_key(r, hf);
+                pv[r] = (qr < S && kj < S) ? pcol[(int64_t)qr * S] : 0.f;
+            }
+        };
+        // The wave's tiles are it = it0 + st*NQS + qsp for st = 0, 1, ...;
+        // the next one's P is requested while this one's MFMAs run.
+        floatx16 pnext;
+        {
+            int it = it0 + qsp;
+            while (it < wit0) it += NQS;
+            if (it < nq) load_p(pnext, it);
+        }
+
         auto compute = [&](int st, const float* cur) {
             const int it = it0 + st * NQS + qsp;
             if (it >= nq || it < wit0) return;
             const float* tile = cur + qsp * QT;
             floatx16 x[2];  // [0] = P, [1] = dS, register r <-> query it*32 + acc_key(r, h)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int qr = it * BK + acc_key(r, hf);
-                x[0][r] = (qr < S && kj < S) ? pcol[(int64_t)qr * S] : 0.f;
-            }
+            x[0] = pnext;
+            if (it + NQS < nq) load_p(pnext, it + NQS);
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
