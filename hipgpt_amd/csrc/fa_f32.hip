@@ -28,7 +28,7 @@ namespace {
 
 using fa::BK;
 
-template <int DP_>
+template <int DP_, bool VPRE_ = (DP_ <= 32)>
 struct F32Traits {
     static constexpr int DP = DP_;
     using elem = float;
@@ -108,9 +108,13 @@ struct F32Traits {
 
     // V^T operands of a tile: lane (c, hf) of block db needs
     // V[acc_key(t, hf)][db*32 + c], t = 0..15 -- four ds_read_b128 per block.
-    // For DP <= 64 they are read before the softmax (VReg holds them); at
-    // DP = 128 registers are short and each block is read just before use.
-    static constexpr bool VPRE = DP <= 64;
+    // VPRE: read before the softmax (VReg holds them) -- the streaming kernel
+    // at DP = 32 and the resident kernel; otherwise each block is read just
+    // before use.  That brings the streaming kernel at DP = 64 to 128 VGPRs:
+    // with WAVES_PER_EU = 4 two 8-wave workgroups share a CU (c3: 132 -> 128
+    // us; prefetching V under the same cap spills).
+    static constexpr bool VPRE = VPRE_;
+    static constexpr int WAVES_PER_EU = (DP == 64 && !VPRE) ? 4 : 1;
     struct VReg {
         floatx4 v[VPRE ? DP / 32 : 1][4];
         const float* vt;
@@ -213,8 +217,8 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
         if (a.D == 32 && fa::resident_lds_bytes<F32Traits<32>, 8, HIPGPT_RES_D32_NKS>(a) != 0)
             return fa::launch_resident<F32Traits<32>, 8, HIPGPT_RES_D32_NKS, 4>(a, causal, stream);
 #endif
-        if (a.D == 64 && fa::resident_lds_bytes<F32Traits<64>, 8, 1>(a) != 0)
-            return fa::launch_resident<F32Traits<64>, 8, 1, 4>(a, causal, stream);
+        if (a.D == 64 && fa::resident_lds_bytes<F32Traits<64, true>, 8, 1>(a) != 0)
+            return fa::launch_resident<F32Traits<64, true>, 8, 1, 4>(a, causal, stream);
     }
     switch (fa_f32_padded_dim(a.D)) {
         case 32:

@@ -390,8 +390,18 @@ struct FaKernel {
     }
 };
 
+// Minimum waves per SIMD the register allocator must allow (traits may set
+// WAVES_PER_EU; 1 = no constraint).  Applied to the 16-byte-load (VEC)
+// instances only: the guarded-load instances of padded head dims need a few
+// more registers and would spill under it.
+template <class TR, class = void>
+struct waves_per_eu { static constexpr int value = 1; };
+template <class TR>
+struct waves_per_eu<TR, std::void_t<decltype(TR::WAVES_PER_EU)>> { static constexpr int value = TR::WAVES_PER_EU; };
+
 template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
-__global__ __launch_bounds__(NQS* NKS * 64) void fa_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NQS* NKS * 64) __attribute__((amdgpu_waves_per_eu(VEC ? waves_per_eu<TR>::value : 1)))
+void fa_fwd_kernel(AttnArgs a) {
     using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>;
     __shared__ __attribute__((aligned(16))) unsigned char lds[K::LDS_BYTES];
     __shared__ int simd_slots[NQS * NKS];
