@@ -48,6 +48,11 @@ CONFIGS = {
     "c1_bwd": (32, 8, 256, 256, 32, True, "f32", True, "bwd"),
     "c1_bwd_legacy": (32, 8, 256, 256, 32, False, "f32", True, "bwd"),
     "c2_bwd": (32, 8, 256, 256, 64, True, "f32", True, "bwd"),
+    # The probs-free training pair at the same shapes: forward writing O and the
+    # row log-sum-exp, and the backward that recomputes P from it.
+    "c1_fwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "fwd_lse"),
+    "c1_bwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "bwd_lse"),
+    "c2_bwd_lse": (32, 8, 256, 256, 64, True, "f32", False, "bwd_lse"),
     # The projections either side of the attention (launch_matmul_add_bias,
     # src/transformer_layer.cpp:217, :220) as (M, N, K, -, -, ...): the c1
     # layer (T = 8192 tokens, E = 256) and the GPT-2-small c3 layer (E = 768).
@@ -76,6 +81,14 @@ def work(cfg):
         # Q, K, V, dO; write dQ, dK, dV
         pairs = Sq * (Sq + 1) // 2 if causal else Sq * Sk
         return 8.0 * B * H * D * pairs, 4 * B * H * (pairs + 7 * Sq * D)
+    if kind == "bwd_lse":
+        # dP, dV, dQ, dK: 8 D flops per visible pair; read Q, K, V, O, dO and
+        # the lse; write dQ, dK, dV
+        pairs = Sq * (Sq + 1) // 2 if causal else Sq * Sk
+        return 8.0 * B * H * D * pairs, 4 * B * H * (8 * Sq * D + Sq)
+    if kind == "fwd_lse":  # the forward's bytes plus the lse row
+        pairs = Sq * (Sq + 1) // 2 if causal else Sq * Sk
+        return 4.0 * B * H * D * pairs, 4 * B * H * (4 * Sq * D + Sq)
     if kind == "kvcache":
         # read the 2047 cached rows and the new row, q; write the new row into
         # the cache and O
@@ -154,6 +167,19 @@ def make_call(cfg, torch, A, dev):
         ws = torch.empty(B * H * Sq, device=dev)
         return (lambda: A.attention_backward(go, qkv, p, grad, B, Sq, E, H, causal=True, workspace=ws),
                 {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_bwd_qkv_planar"})
+    if kind in ("fwd_lse", "bwd_lse"):
+        qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)
+        out = torch.empty(B * Sq, E, device=dev)
+        lse = torch.empty(B * H * Sq, device=dev)
+        A.fwd_lse_qkv_planar(qkv, out, lse, B, Sq, E, H, causal=causal)
+        if kind == "fwd_lse":
+            return (lambda: A.fwd_lse_qkv_planar(qkv, out, lse, B, Sq, E, H, causal=causal),
+                    {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_fwd_lse_qkv_planar"})
+        go = torch.randn(B * Sq * E, device=dev, generator=g)
+        grad = torch.empty(3 * B * Sq * E, device=dev)
+        ws = torch.empty(B * H * Sq, device=dev)
+        return (lambda: A.bwd_lse_qkv_planar(go, qkv, out, lse, grad, B, Sq, E, H, causal=causal, workspace=ws),
+                {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_bwd_lse_qkv_planar"})
     if dtype == "f32" and Sq == Sk:
         # the reference's planar [Q|K|V] buffer
         qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)

@@ -43,6 +43,9 @@ SIGNATURES = {
     "hipgpt_attn_bwd_qkv_planar": (
         _int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]),
     "hipgpt_attn_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
+    "hipgpt_attn_fwd_lse_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
+    "hipgpt_attn_bwd_lse_qkv_planar": (
+        _int, [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]),
     "hipgpt_attn_fwd": (
         _int,
         [_vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int]

@@ -7,6 +7,11 @@ provider here); every call goes through the C ABI to the HIP kernels.
   (``include/hip_kernels.h:39-43``, ``src/hip_kernels.cpp:404-451``): planar
   ``d_qkv = [Q|K|V]`` each ``[B*S, E]``, non-causal, probs written when given.
 * :func:`qkv_planar` -- same layout, plus causal masking and a stream.
+* :func:`launch_multihead_attention_backward` / :func:`attention_backward` --
+  HipGPT's backward on the stored probs.
+* :func:`fwd_lse_qkv_planar` / :func:`bwd_lse_qkv_planar` -- the training pair
+  without a probs buffer: the forward keeps a per-row log-sum-exp and the
+  backward recomputes P from it.
 * :func:`attention` -- strided ``[B, S, H, D]`` views, fp32 or bf16 inputs.
 * :func:`decode` -- one query row per sequence against ``kv_len`` keys,
   split-KV.
@@ -146,6 +151,38 @@ def qkv_planar(d_qkv, d_output, d_attn_probs, B, S, E, H, causal=False, stream=N
         _stream(stream),
     )
     _lib.check(rc, "hipgpt_attn_qkv_planar")
+
+
+def fwd_lse_qkv_planar(d_qkv, d_output, lse, B, S, E, H, causal=False, stream=None):
+    """Training forward without probs: O and the row log-sum-exp
+    ``lse`` [B, H, S] (natural log of the softmax denominator of q.k/sqrt(D))."""
+    _need_cuda("d_qkv", d_qkv, torch.float32)
+    _need_cuda("d_output", d_output, torch.float32)
+    _need_cuda("lse", lse, torch.float32)
+    _need_numel("d_qkv", d_qkv, 3 * B * S * E)
+    _need_numel("d_output", d_output, B * S * E)
+    _need_numel("lse", lse, B * H * S)
+    rc = _lib.lib().hipgpt_attn_fwd_lse_qkv_planar(
+        _ptr(d_qkv), _ptr(d_output), _ptr(lse), B, S, E, H, int(bool(causal)), _stream(stream))
+    _lib.check(rc, "hipgpt_attn_fwd_lse_qkv_planar")
+
+
+def bwd_lse_qkv_planar(grad_out, qkv, out, lse, grad_qkv, B, S, E, H, causal=False, workspace=None, stream=None):
+    """Backward of :func:`fwd_lse_qkv_planar` from its ``out`` and ``lse``
+    (P recomputed per tile; no probs buffer)."""
+    n = B * S * E
+    for name, t, k in (("grad_out", grad_out, n), ("qkv", qkv, 3 * n), ("out", out, n), ("lse", lse, B * H * S),
+                       ("grad_qkv", grad_qkv, 3 * n)):
+        _need_cuda(name, t, torch.float32)
+        _need_numel(name, t, k)
+    need = int(_lib.lib().hipgpt_attn_bwd_workspace_bytes(B, S, H))
+    if workspace is None:
+        workspace = torch.empty(max(1, need // 4), device=qkv.device, dtype=torch.float32)
+    rc = _lib.lib().hipgpt_attn_bwd_lse_qkv_planar(
+        _ptr(grad_out), _ptr(qkv), _ptr(out), _ptr(lse), _ptr(grad_qkv), B, S, E, H, int(bool(causal)),
+        _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream))
+    _lib.check(rc, "hipgpt_attn_bwd_lse_qkv_planar")
+    return grad_qkv
 
 
 def _bshd_strides(t, name):

@@ -270,6 +270,32 @@ int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv, const fl
     return from_hip(hipgpt::launch_attn_bwd(a, stream));
 }
 
+int hipgpt_attn_fwd_lse_qkv_planar(const float* d_qkv, float* d_output, float* lse, int B, int S, int E, int H,
+                                   int causal, hipStream_t stream) {
+    if (!d_qkv || !d_output || !lse || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0) return HIPGPT_ERR_INVALID;
+    const int D = E / H;
+    if ((D != 32 && D != 64) || E % 4 != 0 || !aligned16(d_qkv) || !aligned16(d_output))
+        return HIPGPT_ERR_UNSUPPORTED;
+    AttnArgs a = planar_args(d_qkv, d_output, nullptr, B, S, E, H);
+    a.lse = lse;
+    return attn_dispatch(a, causal, HIPGPT_F32, stream);
+}
+
+int hipgpt_attn_bwd_lse_qkv_planar(const float* grad_out, const float* qkv, const float* out, const float* lse,
+                                   float* grad_qkv, int B, int S, int E, int H, int causal, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+    if (!grad_out || !qkv || !out || !lse || !grad_qkv || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0)
+        return HIPGPT_ERR_INVALID;
+    if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if (!workspace || workspace_bytes < hipgpt_attn_bwd_workspace_bytes(B, S, H)) return HIPGPT_ERR_WORKSPACE;
+    hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, nullptr, grad_qkv, B, S, E, H, causal ? 1 : 0);
+    a.o = out;
+    a.lse = lse;
+    a.dvec = static_cast<float*>(workspace);
+    if (!hipgpt::bwd_tiled_ok(a)) return HIPGPT_ERR_UNSUPPORTED;
+    return from_hip(hipgpt::launch_attn_bwd(a, stream));
+}
+
 int hipgpt_attn_qkv_planar(const float* d_qkv, float* d_output, float* d_attn_probs, int B, int S, int E,
                            int H, int causal, hipStream_t stream) {
     if (!d_qkv || !d_output || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0) return HIPGPT_ERR_INVALID;

@@ -323,11 +323,13 @@ hipError_t launch_dp(const BwdArgs& a, hipStream_t s) {
 bool bwd_tiled_ok(const BwdArgs& a) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     return (a.D == 32 || a.D == 64) && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) && al(a.k) &&
-           al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) && al(a.probs) &&
+           al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) && al(a.probs) && al(a.o) &&
            ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
 }
 
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
+    // recompute mode (no probs): tiled kernels only
+    if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);

@@ -26,6 +26,12 @@
 // Causal (probs zero above the diagonal) skips key tiles past a query
 // tile's diagonal (query-stationary) and query tiles before a key tile's
 // diagonal (key-stationary).
+// Recompute mode (RECOMP; FlashAttention-2's backward): no probs buffer.  The
+// forward's O and row log-sum-exp give Dq_i = dO_i . O_i up front (computed by
+// the query-stationary kernel, which then forms dQ = c dS K directly) and P is
+// rebuilt per tile as exp2(S' - lse'), S' = (c log2 e) q.k from the operand
+// tiles already in LDS plus a row-major K (resp. Q) tile, with the causal
+// mask applied on the diagonal tiles.
 #pragma once
 
 #include <type_traits>
@@ -121,14 +127,17 @@ __device__ __forceinline__ int role_of(int sr, int rank, int nranks, int nw, boo
 }
 
 // ----------------------------------------------------------------- dQ, Dq
-template <int DP, int NQS, int NKS, bool CAUSAL>
+template <int DP, int NQS, int NKS, bool CAUSAL, bool RECOMP>
 struct BwdQ {
     using T = Tiles<DP>;
     static constexpr int NW = NQS * NKS;
     static constexpr int NT = NW * 64;
     static constexpr int NDB = DP / 32;
-    // stage: NKS key tiles, each V row-major + K transposed
-    static constexpr int STAGE = NKS * (T::ROW + T::TR);
+    static constexpr int NACC = RECOMP ? 1 : 2;  // accumulators: A (, Bm)
+    // stage: NKS key tiles, each V row-major + K transposed (+ K row-major,
+    // the A operand of S^T = K Q^T, when P is recomputed)
+    static constexpr int KT = T::ROW + T::TR + (RECOMP ? T::ROW : 0);
+    static constexpr int STAGE = NKS * KT;
     static constexpr int PER = (2 * NKS * T::CPT + NT - 1) / NT;  // chunks per thread per stage
     static constexpr int MERGE = NW * 64 * (2 * 16 * NDB + 1);
     static constexpr int LDS_FLOATS = 2 * STAGE > MERGE ? 2 * STAGE : MERGE;
@@ -162,6 +171,30 @@ struct BwdQ {
                 for (int j = 0; j < 4; ++j) go[s + j] = t[j];
             }
         }
+        // Recompute mode: Q (B operand of S^T = K Q^T) pre-scaled to log2
+        // units, the row's log-sum-exp in the same units, and the row dot
+        // Dq_i = dO_i . O_i, published once for the key-stationary kernel.
+        float q2[RECOMP ? DP / 2 : 1];
+        float lse2 = 0.f, dqv = 0.f;
+        if constexpr (RECOMP) {
+            const float qsc = a.scale * kLog2e;
+            const float* qp = a.q + base + (int64_t)qi * a.ts + hf * (DP / 2);
+            const float* op = a.o + base + (int64_t)qi * a.ts + hf * (DP / 2);
+            float dsum = 0.f;
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const floatx4 qv = qi < S ? *reinterpret_cast<const floatx4*>(qp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+                const floatx4 ov = qi < S ? *reinterpret_cast<const floatx4*>(op + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    q2[s + j] = qv[j] * qsc;
+                    dsum = fmaf(go[s + j], ov[j], dsum);
+                }
+            }
+            dqv = halves_sum(dsum);
+            if (qi < S) lse2 = a.lse[(int64_t)bh * S + qi] * kLog2e;
+            if (ks == 0 && hf == 0 && qi < S) a.dvec[(int64_t)bh * S + qi] = dqv;
+        }
         RowLoader kl, vl;
         kl.init(a.k + base, a.ts, S, a.D);
         vl.init(a.v + base, a.ts, S, a.D);
@@ -185,23 +218,25 @@ struct BwdQ {
                 const int isk = f >= NKS * T::CPT;
                 const int g = isk ? f - NKS * T::CPT : f;
                 const int kt = g / T::CPT, r = (g % T::CPT) / T::CPR, cc = g % T::CPR;
-                float* tile = dst + kt * (T::ROW + T::TR);
-                if (isk)
+                float* tile = dst + kt * KT;
+                if (isk) {
                     T::store_tr(tile + T::ROW, r, cc, stg[i]);
-                else
+                    if (RECOMP) T::store_row(tile + T::ROW + T::TR, r, cc, stg[i]);
+                } else {
                     T::store_row(tile, r, cc, stg[i]);
+                }
             }
         };
 
-        floatx16 acc[2][NDB];  // [0] = A^T, [1] = Bm^T, both [d][query]
+        floatx16 acc[NACC][NDB];  // [0] = A^T (recompute: dS K, unscaled), [1] = Bm^T, both [d][query]
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+        for (int n = 0; n < NACC; ++n)
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
         float ld = 0.f;
-        const float* prow = a.probs + ((int64_t)bh * S + qi) * S;
+        const float* prow = RECOMP ? nullptr : a.probs + ((int64_t)bh * S + qi) * S;
         const bool pvec = (S & 3) == 0;
 
         // P of key tile t in accumulator order: piece g holds keys
@@ -220,30 +255,51 @@ struct BwdQ {
         };
         // The next tile's P is requested while this tile's MFMAs run.
         floatx4 pnext[4];
-        if (ks < wtiles) load_p(pnext, ks);
+        if (!RECOMP && ks < wtiles) load_p(pnext, ks);
 
         auto compute = [&](int st, const float* cur) {
             const int t = st * NKS + ks;
             if (t >= wtiles) return;
-            const float* tile = cur + ks * (T::ROW + T::TR);
+            const float* tile = cur + ks * KT;
             floatx16 x[2];
+            if constexpr (RECOMP) {
+                floatx16 sc;
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
+                for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+                T::dchain(sc, tile + T::ROW + T::TR, q2, c, hf);  // S'^T, register r <-> key acc_key(r, h)
+                const int kb0 = t * BK;
+                const bool edge = kb0 + BK > S || (CAUSAL && kb0 + BK - 1 > qw0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) x[1][4 * g + j] = pnext[g][j];
-            if (t + NKS < wtiles) load_p(pnext, t + NKS);
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb0 + acc_key(r, hf);
+                    const float p = fast_exp2(sc[r] - lse2);
+                    x[1][r] = (!edge || (key < S && (!CAUSAL || key <= qi))) ? p : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) x[1][4 * g + j] = pnext[g][j];
+                if (t + NKS < wtiles) load_p(pnext, t + NKS);
+            }
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
             T::dchain(dp, tile, go, c, hf);  // dP^T, register r <-> key acc_key(r, h)
-            float s = 0.f;
+            if constexpr (RECOMP) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                x[0][r] = x[1][r] * dp[r];
-                s += x[0][r];
+                for (int r = 0; r < 16; ++r) x[0][r] = x[1][r] * (dp[r] - dqv);
+                T::template rchain<1>(acc, tile + T::ROW, x, c, hf);  // (dS K)^T += K^T dS^T
+            } else {
+                float s = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    x[0][r] = x[1][r] * dp[r];
+                    s += x[0][r];
+                }
+                ld += s;
+                T::template rchain<2>(acc, tile + T::ROW, x, c, hf);  // A^T += K^T (P o dP)^T, Bm^T += K^T P^T
             }
-            ld += s;
-            T::template rchain<2>(acc, tile + T::ROW, x, c, hf);  // A^T += K^T (P o dP)^T, Bm^T += K^T P^T
         };
 
         if (nstages > 0) {
@@ -264,7 +320,7 @@ struct BwdQ {
             constexpr int W = 2 * 16 * NDB + 1;
             if (ks != 0) {
 #pragma unroll
-                for (int n = 0; n < 2; ++n)
+                for (int n = 0; n < NACC; ++n)
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -276,7 +332,7 @@ struct BwdQ {
 #pragma unroll
                 for (int j = 1; j < NKS; ++j) {
 #pragma unroll
-                    for (int n = 0; n < 2; ++n)
+                    for (int n = 0; n < NACC; ++n)
 #pragma unroll
                         for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -287,8 +343,8 @@ struct BwdQ {
             }
         }
         if (ks == 0 && qi < S) {
-            const float dq = halves_sum(ld);
-            if (hf == 0) a.dvec[(int64_t)bh * S + qi] = dq;
+            const float dq = RECOMP ? dqv : halves_sum(ld);
+            if (!RECOMP && hf == 0) a.dvec[(int64_t)bh * S + qi] = dq;
             float* out = a.dq + base + (int64_t)qi * a.ts;
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
@@ -297,7 +353,8 @@ struct BwdQ {
                     floatx4 v;
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        v[j] = a.scale * fmaf(-dq, acc[1][db][4 * g + j], acc[0][db][4 * g + j]);
+                        v[j] = RECOMP ? a.scale * acc[0][db][4 * g + j]
+                                      : a.scale * fmaf(-dq, acc[NACC - 1][db][4 * g + j], acc[0][db][4 * g + j]);
                     *reinterpret_cast<floatx4*>(out + db * 32 + 8 * g + 4 * hf) = v;
                 }
         }
@@ -305,14 +362,19 @@ struct BwdQ {
 };
 
 // ----------------------------------------------------------------- dK, dV
-template <int DP, int NKB, int NQS, bool CAUSAL>
+template <int DP, int NKB, int NQS, bool CAUSAL, bool RECOMP>
 struct BwdKV {
     using T = Tiles<DP>;
     static constexpr int NW = NKB * NQS;
     static constexpr int NT = NW * 64;
     static constexpr int NDB = DP / 32;
-    // stage: NQS query tiles, each dO row-major + dO transposed + Q transposed + Dq
-    static constexpr int QT = T::ROW + 2 * T::TR + BK;
+    // stage: NQS query tiles, each dO row-major + dO transposed + Q transposed
+    // + Dq (+ lse' + Q row-major, the A operand of S' = Q K^T, when P is
+    // recomputed)
+    static constexpr int DQ_OFF = T::ROW + 2 * T::TR;
+    static constexpr int LSE_OFF = DQ_OFF + BK;
+    static constexpr int QROW_OFF = LSE_OFF + BK;
+    static constexpr int QT = DQ_OFF + BK + (RECOMP ? BK + T::ROW : 0);
     static constexpr int STAGE = NQS * QT;
     static constexpr int PER = (2 * NQS * T::CPT + NT - 1) / NT;
     static constexpr int MERGE = NW * 64 * (2 * 16 * NDB);
@@ -348,11 +410,24 @@ struct BwdKV {
                 for (int j = 0; j < 4; ++j) vr[s + j] = t[j];
             }
         }
+        // Recompute mode: K (B operand of S' = Q K^T) pre-scaled to log2 units
+        float kr2[RECOMP ? DP / 2 : 1];
+        if constexpr (RECOMP) {
+            const float qsc = a.scale * kLog2e;
+            const float* kp = a.k + base + (int64_t)kj * a.ts + hf * (DP / 2);
+#pragma unroll
+            for (int s = 0; s < DP / 2; s += 4) {
+                const floatx4 t = kj < S ? *reinterpret_cast<const floatx4*>(kp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kr2[s + j] = t[j] * qsc;
+            }
+        }
         RowLoader gl, ql;
         gl.init(a.go + base, a.ts, S, a.D);
         ql.init(a.q + base, a.ts, S, a.D);
         floatx4 stg[PER];
-        float dqs = 0.f;  // Dq value this thread stages
+        float dqs = 0.f;   // Dq value this thread stages
+        float lses = 0.f;  // lse' value this thread stages (+inf past the last row: P = 0)
         auto load = [&](int st) {
             const int qt0 = it0 + st * NQS;
 #pragma unroll
@@ -367,6 +442,7 @@ struct BwdKV {
             if (tid < NQS * BK) {
                 const int qrow = qt0 * BK + tid;
                 dqs = qrow < S ? a.dvec[(int64_t)bh * S + qrow] : 0.f;
+                if (RECOMP) lses = qrow < S ? a.lse[(int64_t)bh * S + qrow] * kLog2e : kInf;
             }
         };
         auto store = [&](float* dst) {
@@ -380,12 +456,16 @@ struct BwdKV {
                 float* tile = dst + qt * QT;
                 if (isq) {
                     T::store_tr(tile + T::ROW + T::TR, r, cc, stg[i]);
+                    if (RECOMP) T::store_row(tile + QROW_OFF, r, cc, stg[i]);
                 } else {
                     T::store_row(tile, r, cc, stg[i]);
                     T::store_tr(tile + T::ROW, r, cc, stg[i]);
                 }
             }
-            if (tid < NQS * BK) dst[(tid / BK) * QT + T::ROW + 2 * T::TR + tid % BK] = dqs;
+            if (tid < NQS * BK) {
+                dst[(tid / BK) * QT + DQ_OFF + tid % BK] = dqs;
+                if (RECOMP) dst[(tid / BK) * QT + LSE_OFF + tid % BK] = lses;
+            }
         };
 
         floatx16 acc[2][NDB];  // [0] = dV^T, [1] = dK^T (unscaled), both [d][key]
@@ -395,7 +475,7 @@ struct BwdKV {
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
-        const float* pcol = a.probs + (int64_t)bh * S * S + kj;
+        const float* pcol = RECOMP ? nullptr : a.probs + (int64_t)bh * S * S + kj;
 
         // P column of query tile it, register r <-> query it*32 + acc_key(r, h)
         auto load_p = [&](floatx16& pv, int it) {
@@ -408,7 +488,7 @@ struct BwdKV {
         // The wave's tiles are it = it0 + st*NQS + qsp for st = 0, 1, ...;
         // the next one's P is requested while this one's MFMAs run.
         floatx16 pnext;
-        {
+        if (!RECOMP) {
             int it = it0 + qsp;
             while (it < wit0) it += NQS;
             if (it < nq) load_p(pnext, it);
@@ -419,13 +499,32 @@ struct BwdKV {
             if (it >= nq || it < wit0) return;
             const float* tile = cur + qsp * QT;
             floatx16 x[2];  // [0] = P, [1] = dS, register r <-> query it*32 + acc_key(r, h)
-            x[0] = pnext;
-            if (it + NQS < nq) load_p(pnext, it + NQS);
+            if constexpr (RECOMP) {
+                floatx16 sc;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+                T::dchain(sc, tile + QROW_OFF, kr2, c, hf);  // S', register r <-> query acc_key(r, h)
+                const float* lt = tile + LSE_OFF;
+                // causal: some query of this tile precedes some key of the wave
+                const bool edge = CAUSAL && it * BK < kw0 + BK - 1;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const floatx4 l4 = *reinterpret_cast<const floatx4*>(lt + 8 * g + 4 * hf);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float p = fast_exp2(sc[4 * g + j] - l4[j]);
+                        x[0][4 * g + j] = (!edge || it * BK + acc_key(4 * g + j, hf) >= kj) ? p : 0.f;
+                    }
+                }
+            } else {
+                x[0] = pnext;
+                if (it + NQS < nq) load_p(pnext, it + NQS);
+            }
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
             T::dchain(dp, tile, vr, c, hf);  // dP, register r <-> query acc_key(r, h)
-            const float* dqt = tile + T::ROW + 2 * T::TR;
+            const float* dqt = tile + DQ_OFF;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const floatx4 dq = *reinterpret_cast<const floatx4*>(dqt + 8 * g + 4 * hf);
@@ -491,44 +590,47 @@ struct BwdKV {
     }
 };
 
-template <int DP, int NQS, int NKS, bool CAUSAL>
+template <int DP, int NQS, int NKS, bool CAUSAL, bool RECOMP>
 __global__ __launch_bounds__(NQS* NKS * 64) void bwd_q_kernel(BwdArgs a, int nqb) {
-    using K = BwdQ<DP, NQS, NKS, CAUSAL>;
+    using K = BwdQ<DP, NQS, NKS, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     __shared__ int simd_slots[NQS * NKS];
     K::run(a, lds, simd_slots, nqb);
 }
 
-template <int DP, int NKB, int NQS, bool CAUSAL>
+template <int DP, int NKB, int NQS, bool CAUSAL, bool RECOMP>
 __global__ __launch_bounds__(NKB* NQS * 64) void bwd_kv_kernel(BwdArgs a, int nkb) {
-    using K = BwdKV<DP, NKB, NQS, CAUSAL>;
+    using K = BwdKV<DP, NKB, NQS, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     __shared__ int simd_slots[NKB * NQS];
     K::run(a, lds, simd_slots, nkb);
 }
 
 // Both kernels for one problem (the second reads the first's Dq).
-template <int DP, int QNQS, int QNKS, int KNKB, int KNQS>
-hipError_t launch_tiled(const BwdArgs& a, hipStream_t s) {
+template <int DP, int QNQS, int QNKS, int KNKB, int KNQS, bool CAUSAL, bool RECOMP>
+hipError_t launch_tiled_mode(const BwdArgs& a, hipStream_t s) {
     const int BH = a.B * a.H;
     const int nqb = (a.S + QNQS * BK - 1) / (QNQS * BK);
     const int nkb = (a.S + KNKB * BK - 1) / (KNKB * BK);
     const int64_t g1 = (int64_t)nqb * BH, g2 = (int64_t)nkb * BH;
     if (g1 <= 0 || g1 > 0x7fffffff || g2 > 0x7fffffff) return hipErrorInvalidConfiguration;
-    if (a.causal)
-        hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, true>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s, a, nqb);
-    else
-        hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, false>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s, a,
-                           nqb);
+    hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, CAUSAL, RECOMP>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s,
+                       a, nqb);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (a.causal)
-        hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, true>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0, s, a,
-                           nkb);
-    else
-        hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, false>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0, s, a,
-                           nkb);
+    hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, CAUSAL, RECOMP>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0,
+                       s, a, nkb);
     return hipGetLastError();
+}
+
+template <int DP, int QNQS, int QNKS, int KNKB, int KNQS>
+hipError_t launch_tiled(const BwdArgs& a, hipStream_t s) {
+    const bool recomp = a.probs == nullptr;
+    if (a.causal)
+        return recomp ? launch_tiled_mode<DP, QNQS, QNKS, KNKB, KNQS, true, true>(a, s)
+                      : launch_tiled_mode<DP, QNQS, QNKS, KNKB, KNQS, true, false>(a, s);
+    return recomp ? launch_tiled_mode<DP, QNQS, QNKS, KNKB, KNQS, false, true>(a, s)
+                  : launch_tiled_mode<DP, QNQS, QNKS, KNKB, KNQS, false, false>(a, s);
 }
 
 }  // namespace bwd

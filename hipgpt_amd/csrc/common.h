@@ -13,7 +13,9 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kInf = __builtin_inff();
 // Running-max start value.  Finite (unlike -inf) so that the first rescale
 // exp2(m_old - m_new) is exp2(-huge) = 0 rather than exp2(-inf + inf) = NaN;
 // the same value the reference starts from (src/hip_kernels.cpp:279, :350).
@@ -43,6 +45,7 @@ struct AttnArgs {
     int causal_off;  // causal: query i sees keys j <= i + causal_off (Sk - Sq)
     float qscale;    // softmax scale * log2(e), folded into Q
     int n_qblk;      // query blocks per (b,h)
+    float* lse;      // optional [B*H][Sq]: ln sum_j exp(scale * q_i . k_j) over visible keys
 };
 
 // exp2 on the transcendental unit (v_exp_f32): exp2(-inf) = 0.

@@ -212,7 +212,7 @@ int fa_f32_padded_dim(int D) {
 
 hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t stream) {
     const bool probs = a.probs != nullptr;
-    if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ) {
+    if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ && !a.lse) {  // the resident kernel writes no lse
 #if HIPGPT_RES_D32_NKS > 0
         if (a.D == 32 && fa::resident_lds_bytes<F32Traits<32>, 8, HIPGPT_RES_D32_NKS>(a) != 0)
             return fa::launch_resident<F32Traits<32>, 8, HIPGPT_RES_D32_NKS, 4>(a, causal, stream);

@@ -304,6 +304,7 @@ struct FaKernel {
 #pragma unroll
                     for (int j = 1; j < NKS; ++j) M = fmaxf(M, m_slot[(role + j) * 64 + lane]);
                     const float w0 = fast_exp2(m_run - M);
+                    m_run = M;
                     l_run *= w0;
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
@@ -367,6 +368,10 @@ struct FaKernel {
         }
 
         // ---------------- epilogue: O = O^T / l (wave ks == 0) ----------------
+        // Row log-sum-exp (natural log) when asked for (no-probs path only):
+        // scores are in log2 units of scale * q.k, l = sum 2^(s - m).
+        if (!PROBS && a.lse && ks == 0 && hf == 0 && qi < Sq)
+            a.lse[(int64_t)bh * Sq + qi] = (m_run + log2f(l_run)) * kLn2;
         if (ks == 0 && qi < Sq) {
             const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;

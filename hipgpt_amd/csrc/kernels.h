@@ -48,12 +48,19 @@ hipError_t launch_decode(const AttnArgs& a, int dtype, int nsplit, float* ws, hi
 struct BwdArgs {
     const float *q, *k, *v, *go, *probs;
     float *dq, *dk, *dv, *dvec;
+    // Recompute mode (probs == nullptr): the forward's output O and row
+    // log-sum-exp lse [B*H][S] (natural log); P is rebuilt per tile as
+    // exp(scale q.k - lse) and dvec receives the row dots dO . O.
+    const float *o, *lse;
     int64_t bs, ts, hs;
     int B, H, S, D;
     int causal;
     float scale;
 };
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s);
+// The LDS-tiled MFMA kernels apply (D = 32 or 64, 16-byte aligned rows); the
+// only backward path for recompute mode.
+bool bwd_tiled_ok(const BwdArgs& a);
 
 // Unfused single-head helpers (HipGPT src/hip_kernels.cpp:454-532).
 hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int S, int D, hipStream_t s);

@@ -65,6 +65,27 @@ int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv,
                                void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
 
+/* Training pair without the [B][H][S][S] probs buffer (FlashAttention-2's
+ * forward/backward split).  No counterpart in HipGPT, whose backward reads the
+ * stored probs (src/hip_kernels.cpp:1159-1272); this pair computes the same
+ * gradients from O and a per-row log-sum-exp instead.
+ *   forward:  planar buffers as hipgpt_attn_qkv_planar, plus
+ *             lse [B][H][S] = ln sum_j exp(q_i . k_j / sqrt(D)) over the keys
+ *             query i sees (all, or j <= i when causal).
+ *   backward: grad_out, qkv, the forward's out and lse -> every element of
+ *             the planar grad_qkv [dQ|dK|dV]; P is recomputed per tile.
+ *             workspace: hipgpt_attn_bwd_workspace_bytes(B, S, H).
+ * fp32, D = E/H of 32 or 64, 16-byte aligned buffers; other shapes return
+ * HIPGPT_ERR_UNSUPPORTED. */
+int hipgpt_attn_fwd_lse_qkv_planar(const float* d_qkv, float* d_output,
+                                   float* lse, int B, int S, int E, int H,
+                                   int causal, hipStream_t stream);
+int hipgpt_attn_bwd_lse_qkv_planar(const float* grad_out, const float* qkv,
+                                   const float* out, const float* lse,
+                                   float* grad_qkv, int B, int S, int E, int H,
+                                   int causal, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+
 /* HipGPT's planar [3][B*S][E] layout with the options the legacy symbol
  * lacks: causal masking (keys j <= i; probs written 0 above the diagonal so
  * HipGPT's backward, src/hip_kernels.cpp:1162-1243, stays exact) and a
