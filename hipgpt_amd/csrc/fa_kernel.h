@@ -152,7 +152,17 @@ struct FaKernel {
         // waves ranked by SIMD gives each SIMD a different role in each of
         // the co-resident workgroups, evening out causal work.  Roles are
         // wave-uniform (scalar registers), so tile indexing stays scalar.
-        const int role = (simd_rank<NW>(simd_slots, wave, lane) + rank) % NW;
+        const int sr = simd_rank<NW>(simd_slots, wave, lane);
+        int role = (sr + rank) % NW;
+        if (CAUSAL && NW == 8) {
+            // Two waves per SIMD: the second takes the mirror (NQS-1-qs,
+            // NKS-1-ks) of the first's role, so in the diagonal stages, where
+            // sub-block qs stops after its own diagonal tile, the waves still
+            // busy sit on different SIMDs (c3 128.4 -> 127.1 us, c4 604 -> 586).
+            const int b = ((sr >> 1) + rank) % 4;
+            const int qb0 = b / NKS, kb0 = b % NKS;
+            role = (sr & 1) ? (NQS - 1 - qb0) * NKS + (NKS - 1 - kb0) : qb0 * NKS + kb0;
+        }
         const int qs = role / NKS;
         const int ks = role % NKS;
         const int b = bh / a.H;
