@@ -115,6 +115,9 @@ struct F32Traits {
     // us; prefetching V under the same cap spills).
     static constexpr bool VPRE = VPRE_;
     static constexpr int WAVES_PER_EU = (DP == 64 && !VPRE) ? 4 : 1;
+    // With probs at DP = 32, rows of up to 4 stages (Sk <= 256 at two key
+    // splits) keep their score tiles in registers between the two sweeps.
+    static constexpr int PROBS_RES_STAGES = DP == 32 ? 4 : 0;
     struct VReg {
         floatx4 v[VPRE ? DP / 32 : 1][4];
         const float* vt;

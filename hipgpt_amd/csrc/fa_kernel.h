@@ -22,6 +22,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "fa_common.h"
@@ -35,7 +36,16 @@ namespace fa {
 constexpr unsigned long long kStaggerTicks = 20;
 constexpr int kStaggerMaxBlocks = 4;
 
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+// Compile-time loop over I = 0 .. N-1 (each body sees I as a constant).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+
+// SRT > 0 (probs only): when a wave's key tiles span at most SRT stages, the
+// max/sum sweep keeps every score tile in registers and the probs sweep reads
+// them back instead of recomputing Q K^T (it stages V only).
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 struct FaKernel {
     static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");
     static constexpr int DP = TR::DP;
@@ -98,14 +108,15 @@ struct FaKernel {
             }
         }
 
-        template <int SL, bool WV = true>
+        template <int SL, bool WV = true, bool WK = true>
         __device__ __forceinline__ void load(int stage, int tid) {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
                 const int f = tid + i * NT;
                 if (VEC) {
                     if (CPS % NT == 0 || f < CPS) {
-                        kr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
+                        if (WK)
+                            kr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
                         if (WV)
                             vr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
                     }
@@ -114,12 +125,12 @@ struct FaKernel {
                     const int cc = f % CPR;
                     const int key = stage * NKS * BK + row;
                     const bool ok = (CPS % NT == 0 || f < CPS) && key < Sk;
-                    kr[SL][i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
+                    if (WK) kr[SL][i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
                     if (WV) vr[SL][i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
                 }
             }
         }
-        template <int SL, bool WV = true>
+        template <int SL, bool WV = true, bool WK = true>
         __device__ __forceinline__ void store(E* stage, int tid) const {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -131,7 +142,7 @@ struct FaKernel {
                 const int r = row % BK;
                 E* Kt = stage + kt * TR::KTILE;
                 E* Vt = stage + NKS * TR::KTILE + kt * TR::VTILE;
-                TR::store_k_chunk(Kt, r, cc, kr[SL][i]);
+                if (WK) TR::store_k_chunk(Kt, r, cc, kr[SL][i]);
                 if (WV) TR::store_vt_chunk(Vt, r, cc, vr[SL][i]);
             }
         }
@@ -291,6 +302,51 @@ struct FaKernel {
             }
         };
 
+        // Score-resident probs sweeps (SRT > 0).  Stage I holds tile I*NKS + ks
+        // of this wave; sres[I] keeps its masked scores between the sweeps.
+        floatx16 sres[SRT > 0 ? SRT : 1];
+        auto sweep_res = [&](auto second_tag, float linv, float* prow, bool pvec) {
+            constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
+            if (nstages > 0) {
+                st.template load<0, SECOND, !SECOND>(0, tid);
+                st.template store<0, SECOND, !SECOND>(lds, tid);
+            }
+            __syncthreads();
+            static_for(
+                [&](auto ic) {
+                    constexpr int I = decltype(ic)::value;
+                    if (I < nstages) {
+                        if (I + 1 < nstages) st.template load<0, SECOND, !SECOND>(I + 1, tid);
+                        const E* cur = lds + (I & 1) * STAGE_ELEMS;
+                        const int t = I * NKS + ks;
+                        if (t < wtiles) {
+                            if (!SECOND) {
+                                const floatx16 sv = tile_scores(cur, t);
+                                sres[I] = sv;
+                                const float m_new = vmax(m_run, tile_max(sv) * sc);
+                                float ls = 0.f;
+#pragma unroll
+                                for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(sv[r], sc, -m_new));
+                                l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
+                                m_run = m_new;
+                            } else {
+                                typename TR::VReg vreg;
+                                TR::load_v(vreg, vt_of(cur, t), c, hf);
+                                floatx16 p = sres[I];
+#pragma unroll
+                                for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -m_run)) * linv;
+                                if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
+                                TR::pv(vreg, p, o, c, hf);
+                            }
+                        }
+                        if (I + 1 < nstages)
+                            st.template store<0, SECOND, !SECOND>(lds + ((I + 1) & 1) * STAGE_ELEMS, tid);
+                        __syncthreads();
+                    }
+                },
+                std::make_integer_sequence<int, (SRT > 0 ? SRT : 1)>{});
+        };
+
         float* const mrg = reinterpret_cast<float*>(lds_raw);  // merge scratch (after a barrier)
         float* const m_slot = mrg;                              // [NW][64]
         float* const l_slot = mrg + NW * 64;                    // [NW][64]
@@ -333,7 +389,10 @@ struct FaKernel {
                 }
             }
         } else {
-            sweep(std::integral_constant<int, 1>{}, 0.f, nullptr, false);
+            if constexpr (SRT > 0)
+                sweep_res(std::false_type{}, 0.f, nullptr, false);
+            else
+                sweep(std::integral_constant<int, 1>{}, 0.f, nullptr, false);
             if (NKS > 1) {
                 m_slot[role * 64 + lane] = m_run;
                 l_slot[role * 64 + lane] = l_run;
@@ -352,7 +411,10 @@ struct FaKernel {
             const float linv = 1.0f / fmaxf(l_run, 1e-20f);
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
             const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
-            sweep(std::integral_constant<int, 2>{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
+            if constexpr (SRT > 0)
+                sweep_res(std::true_type{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
+            else
+                sweep(std::integral_constant<int, 2>{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
             if (CAUSAL && qw0 < Sq && ks == 0) {
                 const int ztile = tr.wtiles;  // tiles [0, wtiles) were written by the NKS waves
                 zero_probs_tail(probs_bh, qw0, Sq, Sk, ztile * BK, lane, pvec);
@@ -414,28 +476,44 @@ struct waves_per_eu { static constexpr int value = 1; };
 template <class TR>
 struct waves_per_eu<TR, std::void_t<decltype(TR::WAVES_PER_EU)>> { static constexpr int value = TR::WAVES_PER_EU; };
 
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 __global__ __launch_bounds__(NQS* NKS * 64) __attribute__((amdgpu_waves_per_eu(VEC ? waves_per_eu<TR>::value : 1)))
 void fa_fwd_kernel(AttnArgs a) {
-    using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>;
+    using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>;
     __shared__ __attribute__((aligned(16))) unsigned char lds[K::LDS_BYTES];
     __shared__ int simd_slots[NQS * NKS];
     K::run(a, lds, simd_slots);
 }
 
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC>
+template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     AttnArgs args = a;
     args.n_qblk = (a.Sq + NQS * QW - 1) / (NQS * QW);
     const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>), dim3((unsigned)grid),
                        dim3(NQS * NKS * 64), 0, stream, args);
     return hipGetLastError();
 }
 
+// Score-resident stages of a traits type (PROBS_RES_STAGES; 0 = the probs
+// sweeps recompute Q K^T).
+template <class TR, class = void>
+struct probs_res_stages { static constexpr int value = 0; };
+template <class TR>
+struct probs_res_stages<TR, std::void_t<decltype(TR::PROBS_RES_STAGES)>> {
+    static constexpr int value = TR::PROBS_RES_STAGES;
+};
+
 template <class TR, int NQS, int NKS, int PF, bool VEC>
 hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
+    constexpr int SRT = probs_res_stages<TR>::value;
+    if constexpr (SRT > 0) {
+        // every wave's key tiles fit the resident stages (Sk <= SRT * NKS * 32)
+        if (probs && ((a.Sk + BK - 1) / BK + NKS - 1) / NKS <= SRT)
+            return causal ? launch_fa<TR, NQS, NKS, PF, true, true, VEC, SRT>(a, s)
+                          : launch_fa<TR, NQS, NKS, PF, false, true, VEC, SRT>(a, s);
+    }
     if (causal)
         return probs ? launch_fa<TR, NQS, NKS, PF, true, true, VEC>(a, s)
                      : launch_fa<TR, NQS, NKS, PF, true, false, VEC>(a, s);
