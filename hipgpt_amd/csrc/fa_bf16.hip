@@ -9,8 +9,9 @@
 //     after scaling.
 //   * O^T = V^T P^T: P is rounded to bf16 (RNE) straight from the score
 //     accumulator; step s uses registers 8s .. 8s+7, i.e. keys
-//     acc_key(8s + j, h), and V^T (72-byte pitch) supplies the same eight
-//     keys as two conflict-free ds_read_b64.
+//     acc_key(8s + j, h).  V is staged row-major (one 16-byte LDS store per
+//     chunk) and the same eight keys of a d column come back transposed by
+//     two ds_read_b64_tr_b16.
 //   * O is accumulated and written in fp32; probs (optional) are fp32.
 // No reference kernel exists for this variant; it computes the reference's
 // function on bf16-rounded inputs.
@@ -35,15 +36,21 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     return r;
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
 template <int D_>
 struct B16Traits {
     static constexpr int DP = D_;
     using elem = u16;
     using chunk = uint4;
     static constexpr int KSTR = DP + 8;  // rows 16*(DP/8+1) bytes apart
-    static constexpr int VTP = BK + 4;   // 72-byte V^T rows
+    // Row-major V rows: a pitch of DP + 16 (8 dwords past a multiple of 32)
+    // puts the four 32-byte row pieces a 16-lane transpose read takes on
+    // disjoint banks.
+    static constexpr int VRP = DP + 16;
     static constexpr int KTILE = BK * KSTR;
-    static constexpr int VTILE = DP * VTP;
+    static constexpr int VTILE = BK * VRP;
 
     struct QReg {
         bf16x8 v[DP / 16];
@@ -67,13 +74,9 @@ struct B16Traits {
     __device__ __forceinline__ static void store_k_chunk(u16* Kt, int r, int cc, const chunk& v) {
         *reinterpret_cast<uint4*>(Kt + r * KSTR + cc * 8) = v;
     }
+    // V stays row-major (key r, head dims 8cc .. 8cc+7); load_v transposes.
     __device__ __forceinline__ static void store_vt_chunk(u16* Vt, int r, int cc, const chunk& v) {
-        const unsigned w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            Vt[(cc * 8 + 2 * j) * VTP + r] = (u16)(w[j] & 0xffffu);
-            Vt[(cc * 8 + 2 * j + 1) * VTP + r] = (u16)(w[j] >> 16);
-        }
+        *reinterpret_cast<uint4*>(Vt + r * VRP + cc * 8) = v;
     }
 
     __device__ __forceinline__ static floatx16 qk(const u16* Kt, const QReg& q, int c, int hf) {
@@ -90,19 +93,26 @@ struct B16Traits {
     }
 
     // V^T operands: step s of block db uses keys acc_key(8s + j, hf), i.e.
-    // V^T[db*32 + c][16s + 4hf + 0..3] and [16s + 8 + 4hf + 0..3].
+    // V[16s + 4hf + 0..3][db*32 + c] and V[16s + 8 + 4hf + 0..3][db*32 + c].
     struct VReg {
         uint4 v[DP / 32][2];
     };
+    // ds_read_b64_tr_b16 (gfx950): in each 16-lane group, lane r supplies
+    // the address of V[k0 + r/4][d0 + 4(r%4) .. +3] and lane i receives
+    // V[k0 + 0..3][d0 + i] (lane layout checked on the MI355X).  Group
+    // (hf, c/16) takes d0 = db*32 + (c & 16) and k0 = 16s + 4hf, +8 for the
+    // second half of step s.
     __device__ __forceinline__ static void load_v(VReg& vr, const u16* Vt, int c, int hf) {
+        const int r = c & 15;
 #pragma unroll
         for (int db = 0; db < DP / 32; ++db) {
-            const u16* p = Vt + (db * 32 + c) * VTP + 4 * hf;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const uint2 lo = *reinterpret_cast<const uint2*>(p + 16 * s);
-                const uint2 hi = *reinterpret_cast<const uint2*>(p + 16 * s + 8);
-                vr.v[db][s] = uint4{lo.x, lo.y, hi.x, hi.y};
+                const u16* p = Vt + (16 * s + 4 * hf + (r >> 2)) * VRP + db * 32 + (c & 16) + 4 * (r & 3);
+                const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p));
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p + 8 * VRP));
+                const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+                vr.v[db][s] = uint4{l2.x, l2.y, h2.x, h2.y};
             }
         }
     }
