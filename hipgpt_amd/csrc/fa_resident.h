@@ -24,6 +24,7 @@
 // same as the streaming kernel's, through the same operand traits.
 #pragma once
 
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -370,12 +371,19 @@ inline size_t resident_lds_bytes(const AttnArgs& a) {
 template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
 hipError_t launch_resident_one(const AttnArgs& args, int ntiles, size_t lds, int64_t grid, hipStream_t stream) {
     auto kern = fa_resident_kernel<TR, NQS, NKS, L, CAUSAL, PROBS>;
-    static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kResidentLdsMax);
+    // The dynamic-LDS limit is a per-device function attribute: raise it once
+    // per device (bit d of attr_set) and instantiation.  Concurrent first calls
+    // may both set it, which is harmless.
+    static std::atomic<unsigned long long> attr_set{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const unsigned long long bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
+    if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kResidentLdsMax);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_set.fetch_or(bit, std::memory_order_release);
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), lds, stream, args, ntiles);
     return hipGetLastError();
