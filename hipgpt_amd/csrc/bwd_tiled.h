@@ -27,11 +27,13 @@
 // tile's diagonal (query-stationary) and query tiles before a key tile's
 // diagonal (key-stationary).
 // Recompute mode (RECOMP; FlashAttention-2's backward): no probs buffer.  The
-// forward's O and row log-sum-exp give Dq_i = dO_i . O_i up front (computed by
-// the query-stationary kernel, which then forms dQ = c dS K directly) and P is
-// rebuilt per tile as exp2(S' - lse'), S' = (c log2 e) q.k from the operand
-// tiles already in LDS plus a row-major K (resp. Q) tile, with the causal
-// mask applied on the diagonal tiles.
+// forward's O and row log-sum-exp give Dq_i = dO_i . O_i up front (each kernel
+// forms it from the dO rows it loads; the query-stationary one then forms
+// dQ = c dS K directly) and P is rebuilt per tile as exp2(S' - lse'),
+// S' = (c log2 e) q.k from the operand tiles already in LDS plus a row-major K
+// (resp. Q) tile, with the causal mask applied on the diagonal tiles.  As
+// neither kernel then reads the other's output, bwd_pair_kernel runs both
+// kinds of workgroup in one launch.
 #pragma once
 
 #include <type_traits>
@@ -139,15 +141,14 @@ struct BwdQ {
     static constexpr int KT = T::ROW + T::TR + (RECOMP ? T::ROW : 0);
     static constexpr int STAGE = NKS * KT;
     static constexpr int PER = (2 * NKS * T::CPT + NT - 1) / NT;  // chunks per thread per stage
-    static constexpr int MERGE = NW * 64 * (2 * 16 * NDB + 1);
+    static constexpr int MERGE = NKS > 1 ? NW * 64 * (2 * 16 * NDB + 1) : 0;
     static constexpr int LDS_FLOATS = 2 * STAGE > MERGE ? 2 * STAGE : MERGE;
 
-    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nqb) {
+    // Workgroup `rank` of the nqb query blocks of problem bh.
+    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nqb, int bh, int rank) {
         const int tid = threadIdx.x, lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31, hf = lane >> 5;
-        const int BH = a.B * a.H;
-        const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
         const int qb = CAUSAL ? nqb - 1 - rank : rank;
         const int role = role_of(fa::simd_rank<NW>(simd_slots, wave, lane), rank, nqb, NW, CAUSAL);
         const int qs = role / NKS, ks = role % NKS;
@@ -173,7 +174,7 @@ struct BwdQ {
         }
         // Recompute mode: Q (B operand of S^T = K Q^T) pre-scaled to log2
         // units, the row's log-sum-exp in the same units, and the row dot
-        // Dq_i = dO_i . O_i, published once for the key-stationary kernel.
+        // Dq_i = dO_i . O_i.
         float q2[RECOMP ? DP / 2 : 1];
         float lse2 = 0.f, dqv = 0.f;
         if constexpr (RECOMP) {
@@ -193,7 +194,6 @@ struct BwdQ {
             }
             dqv = halves_sum(dsum);
             if (qi < S) lse2 = a.lse[(int64_t)bh * S + qi] * kLog2e;
-            if (ks == 0 && hf == 0 && qi < S) a.dvec[(int64_t)bh * S + qi] = dqv;
         }
         RowLoader kl, vl;
         kl.init(a.k + base, a.ts, S, a.D);
@@ -377,15 +377,18 @@ struct BwdKV {
     static constexpr int QT = DQ_OFF + BK + (RECOMP ? BK + T::ROW : 0);
     static constexpr int STAGE = NQS * QT;
     static constexpr int PER = (2 * NQS * T::CPT + NT - 1) / NT;
-    static constexpr int MERGE = NW * 64 * (2 * 16 * NDB);
+    static constexpr int MERGE = NQS > 1 ? NW * 64 * (2 * 16 * NDB) : 0;
     static constexpr int LDS_FLOATS = 2 * STAGE > MERGE ? 2 * STAGE : MERGE;
+    // Recompute mode forms Dq from the staged dO chunks: chunks i < NG of a
+    // thread are dO, and a row's CPR chunks sit in consecutive lanes.
+    static constexpr int NG = NQS * T::CPT / NT;
+    static_assert(!RECOMP || (NQS * T::CPT) % NT == 0, "dO chunks must fill whole passes");
 
-    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nkb) {
+    // Workgroup `rank` (the key block) of the nkb key blocks of problem bh.
+    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int* simd_slots, int nkb, int bh, int rank) {
         const int tid = threadIdx.x, lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31, hf = lane >> 5;
-        const int BH = a.B * a.H;
-        const int bh = blockIdx.x % BH, rank = blockIdx.x / BH;
         const int kb = rank;  // key block; causal: block 0 sees the most query tiles and launches first
         const int role = role_of(fa::simd_rank<NW>(simd_slots, wave, lane), rank, nkb, NW, CAUSAL);
         const int ksub = role / NQS, qsp = role % NQS;
@@ -422,11 +425,13 @@ struct BwdKV {
                 for (int j = 0; j < 4; ++j) kr2[s + j] = t[j] * qsc;
             }
         }
-        RowLoader gl, ql;
+        RowLoader gl, ql, ol;
         gl.init(a.go + base, a.ts, S, a.D);
         ql.init(a.q + base, a.ts, S, a.D);
+        if (RECOMP) ol.init(a.o + base, a.ts, S, a.D);
         floatx4 stg[PER];
-        float dqs = 0.f;   // Dq value this thread stages
+        floatx4 ostg[RECOMP ? NG : 1];  // O chunks matching the dO chunks (recompute mode)
+        float dqs = 0.f;   // Dq value this thread stages (stored-probs mode)
         float lses = 0.f;  // lse' value this thread stages (+inf past the last row: P = 0)
         auto load = [&](int st) {
             const int qt0 = it0 + st * NQS;
@@ -438,11 +443,16 @@ struct BwdKV {
                 const int g = isq ? f - NQS * T::CPT : f;
                 const int row = qt0 * BK + g / T::CPR;
                 stg[i] = isq ? ql.load(row, g % T::CPR) : gl.load(row, g % T::CPR);
+                if constexpr (RECOMP) {
+                    if (i < NG) ostg[i] = ol.load(row, g % T::CPR);
+                }
             }
             if (tid < NQS * BK) {
                 const int qrow = qt0 * BK + tid;
-                dqs = qrow < S ? a.dvec[(int64_t)bh * S + qrow] : 0.f;
-                if (RECOMP) lses = qrow < S ? a.lse[(int64_t)bh * S + qrow] * kLog2e : kInf;
+                if (RECOMP)
+                    lses = qrow < S ? a.lse[(int64_t)bh * S + qrow] * kLog2e : kInf;
+                else
+                    dqs = qrow < S ? a.dvec[(int64_t)bh * S + qrow] : 0.f;
             }
         };
         auto store = [&](float* dst) {
@@ -461,10 +471,24 @@ struct BwdKV {
                     T::store_row(tile, r, cc, stg[i]);
                     T::store_tr(tile + T::ROW, r, cc, stg[i]);
                 }
+                if constexpr (RECOMP) {
+                    // Dq of row r: the chunk dots summed over the row's CPR lanes
+                    // (rows past S load as zero: Dq = 0)
+                    if (i < NG) {
+                        float d = stg[i][0] * ostg[i][0];
+#pragma unroll
+                        for (int j = 1; j < 4; ++j) d = fmaf(stg[i][j], ostg[i][j], d);
+#pragma unroll
+                        for (int m = 1; m < T::CPR; m <<= 1) d += __shfl_xor(d, m);
+                        if (cc == 0) tile[DQ_OFF + r] = d;
+                    }
+                }
             }
             if (tid < NQS * BK) {
-                dst[(tid / BK) * QT + DQ_OFF + tid % BK] = dqs;
-                if (RECOMP) dst[(tid / BK) * QT + LSE_OFF + tid % BK] = lses;
+                if (RECOMP)
+                    dst[(tid / BK) * QT + LSE_OFF + tid % BK] = lses;
+                else
+                    dst[(tid / BK) * QT + DQ_OFF + tid % BK] = dqs;
             }
         };
 
@@ -595,7 +619,8 @@ __global__ __launch_bounds__(NQS* NKS * 64) void bwd_q_kernel(BwdArgs a, int nqb
     using K = BwdQ<DP, NQS, NKS, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     __shared__ int simd_slots[NQS * NKS];
-    K::run(a, lds, simd_slots, nqb);
+    const int BH = a.B * a.H;
+    K::run(a, lds, simd_slots, nqb, blockIdx.x % BH, blockIdx.x / BH);
 }
 
 template <int DP, int NKB, int NQS, bool CAUSAL, bool RECOMP>
@@ -603,24 +628,53 @@ __global__ __launch_bounds__(NKB* NQS * 64) void bwd_kv_kernel(BwdArgs a, int nk
     using K = BwdKV<DP, NKB, NQS, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     __shared__ int simd_slots[NKB * NQS];
-    K::run(a, lds, simd_slots, nkb);
+    const int BH = a.B * a.H;
+    K::run(a, lds, simd_slots, nkb, blockIdx.x % BH, blockIdx.x / BH);
 }
 
-// Both kernels for one problem (the second reads the first's Dq).
+// Recompute mode: the query- and key-stationary workgroups of the same shape
+// in one grid, dealt in chunks of B*H workgroups as query rank 0, key rank 0,
+// query rank 1, ... (the heaviest causal blocks of each kind first), so that
+// both kinds share the CUs -- twice the waves in flight of either kernel
+// alone -- and the pair costs one launch.
+template <int DP, int NQS, int NKS, int NKB, int NQS2, bool CAUSAL>
+__global__ __launch_bounds__(NQS* NKS * 64) void bwd_pair_kernel(BwdArgs a, int nr) {
+    using KQ = BwdQ<DP, NQS, NKS, CAUSAL, true>;
+    using KK = BwdKV<DP, NKB, NQS2, CAUSAL, true>;
+    static_assert(NQS * NKS == NKB * NQS2 && NQS == NKB, "both kinds need the same workgroup and block counts");
+    constexpr int LF = KQ::LDS_FLOATS > KK::LDS_FLOATS ? KQ::LDS_FLOATS : KK::LDS_FLOATS;
+    __shared__ __attribute__((aligned(16))) float lds[LF];
+    __shared__ int simd_slots[NQS * NKS];
+    const int BH = a.B * a.H;
+    const int chunk = blockIdx.x / BH, bh = blockIdx.x % BH;
+    if (chunk & 1)
+        KK::run(a, lds, simd_slots, nr, bh, chunk >> 1);
+    else
+        KQ::run(a, lds, simd_slots, nr, bh, chunk >> 1);
+}
+
+// Both kernels for one problem: stored probs, two launches (the second reads
+// the first's Dq); recompute mode, one launch of the pair kernel.
 template <int DP, int QNQS, int QNKS, int KNKB, int KNQS, bool CAUSAL, bool RECOMP>
 hipError_t launch_tiled_mode(const BwdArgs& a, hipStream_t s) {
     const int BH = a.B * a.H;
     const int nqb = (a.S + QNQS * BK - 1) / (QNQS * BK);
     const int nkb = (a.S + KNKB * BK - 1) / (KNKB * BK);
     const int64_t g1 = (int64_t)nqb * BH, g2 = (int64_t)nkb * BH;
-    if (g1 <= 0 || g1 > 0x7fffffff || g2 > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, CAUSAL, RECOMP>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0, s,
-                       a, nqb);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, CAUSAL, RECOMP>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64), 0,
-                       s, a, nkb);
-    return hipGetLastError();
+    if (g1 <= 0 || g1 + g2 > 0x7fffffff) return hipErrorInvalidConfiguration;
+    if constexpr (RECOMP) {
+        hipLaunchKernelGGL((bwd_pair_kernel<DP, QNQS, QNKS, KNKB, KNQS, CAUSAL>), dim3((unsigned)(g1 + g2)),
+                           dim3(QNQS * QNKS * 64), 0, s, a, nqb);
+        return hipGetLastError();
+    } else {
+        hipLaunchKernelGGL((bwd_q_kernel<DP, QNQS, QNKS, CAUSAL, false>), dim3((unsigned)g1), dim3(QNQS * QNKS * 64), 0,
+                           s, a, nqb);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((bwd_kv_kernel<DP, KNKB, KNQS, CAUSAL, false>), dim3((unsigned)g2), dim3(KNKB * KNQS * 64),
+                           0, s, a, nkb);
+        return hipGetLastError();
+    }
 }
 
 template <int DP, int QNQS, int QNKS, int KNKB, int KNQS>
