@@ -177,8 +177,7 @@ def make_call(cfg, torch, A, dev):
                     {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_fwd_lse_qkv_planar"})
         go = torch.randn(B * Sq * E, device=dev, generator=g)
         grad = torch.empty(3 * B * Sq * E, device=dev)
-        ws = torch.empty(B * H * Sq, device=dev)
-        return (lambda: A.bwd_lse_qkv_planar(go, qkv, out, lse, grad, B, Sq, E, H, causal=causal, workspace=ws),
+        return (lambda: A.bwd_lse_qkv_planar(go, qkv, out, lse, grad, B, Sq, E, H, causal=causal),
                 {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_bwd_lse_qkv_planar"})
     if dtype == "f32" and Sq == Sk:
         # the reference's planar [Q|K|V] buffer

@@ -175,12 +175,10 @@ def bwd_lse_qkv_planar(grad_out, qkv, out, lse, grad_qkv, B, S, E, H, causal=Fal
                        ("grad_qkv", grad_qkv, 3 * n)):
         _need_cuda(name, t, torch.float32)
         _need_numel(name, t, k)
-    need = int(_lib.lib().hipgpt_attn_bwd_workspace_bytes(B, S, H))
-    if workspace is None:
-        workspace = torch.empty(max(1, need // 4), device=qkv.device, dtype=torch.float32)
+    del workspace  # accepted for symmetry with attention_backward; this pair needs none
     rc = _lib.lib().hipgpt_attn_bwd_lse_qkv_planar(
         _ptr(grad_out), _ptr(qkv), _ptr(out), _ptr(lse), _ptr(grad_qkv), B, S, E, H, int(bool(causal)),
-        _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(stream))
+        None, 0, _stream(stream))
     _lib.check(rc, "hipgpt_attn_bwd_lse_qkv_planar")
     return grad_qkv
 

@@ -21,6 +21,7 @@
 // (b, h)) in the operand layouts; the fa_common.h accumulator layout applies.
 // Causal (extended API only) skips tiles of P that lie wholly above the
 // diagonal, where a causal forward wrote zeros.
+#include "bwd_bh.h"
 #include "bwd_tiled.h"
 #include "common.h"
 #include "fa_common.h"
@@ -331,6 +332,7 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     // recompute mode (no probs): tiled kernels only
     if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
+        if (bwd::bh_ok(a)) return bwd::launch_bh(a, s);
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
         return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);

@@ -1,0 +1,289 @@
+// bwd_bh.h -- probs-free attention backward with one workgroup per (b, h),
+// for head dim 32 and S <= 256: the shape of HipGPT's default model
+// (src/train_gpt.cpp:175-180), whose backward is src/hip_kernels.cpp:1159-1272.
+//
+// One (b, h) problem fits one CU: Q and dO rows, the row log-sum-exp and
+// Dq = dO . O stay in LDS for the whole launch, and each of the 8 waves keeps
+// its 32 keys (K, V) in registers.  The wave owning key tile j walks the
+// query tiles (causal: from its diagonal on) and computes per 32x32 tile
+//   S' = (c log2 e) Q K^T,  P = exp2(S' - lse'),  dP = dO V^T,
+//   dS = P o (dP - Dq),  dV^T += dO^T P,  dK^T += Q^T dS,  dQ += dS K,
+// five 32x32x32 products -- the query- and key-stationary kernel pair
+// computes S' and dP twice, seven products.  S' and dP land with one key per
+// lane (queries in the accumulator's register order), the layout dV and dK
+// contract over; dQ contracts over keys, so dS is transposed through a
+// per-wave LDS scratch before the dQ product.
+//
+// The dQ sum over key tiles runs as a chain instead of atomics (a 64-lane
+// ds_add_f32 measured ~650 cycles on gfx950; global float atomics cost ~10 us
+// at c1): at step t the wave of key tile j handles query tile i = j + t
+// (causal; (j + t) mod nt otherwise), so the contributions to tile i arrive
+// from key tiles i, i-1, ..., each one step after the previous.  A wave adds
+// its dQ tile to the partial left in LDS by key tile j+1 (waiting on the
+// tile's counter, which that wave set when it stored the partial), and the
+// last contributor writes the finished rows to global memory.  Every wait is
+// on a wave one step behind in the chain, so all of them end; they are
+// bounded besides.  Each wave stages its own diagonal query tile (Q, dO
+// rows, lse', Dq = dO . O) and flags it, so no workgroup-wide barrier follows
+// the start.  The summation order is fixed: results are deterministic.
+//
+// One launch, no atomics, no workspace; the LDS footprint (145 KB at
+// S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
+// key tiles j and nt-1-j share a SIMD (nt + 1 tiles per SIMD).
+#pragma once
+
+#include <atomic>
+
+#include "bwd_tiled.h"
+#include "common.h"
+#include "fa_common.h"
+#include "kernels.h"
+
+namespace hipgpt {
+namespace bwd {
+namespace bh {
+
+constexpr int D = 32;
+constexpr int NW = 8;          // waves; at most one key tile each
+constexpr int MAXS = NW * BK;  // longest sequence
+constexpr int RP = D + 4;      // pitch of the Q / dO rows
+constexpr int XP = BK + 4;     // pitch of a wave's dS^T scratch ([key][query])
+constexpr int CPR = D / 4;     // 16-byte chunks per row
+
+constexpr int kSpinMax = 1 << 20;  // bound of a flag wait (~0.1 s)
+
+// LDS layout in floats for Sp = S rounded up to 32 rows.
+struct Layout {
+    int q, g, dqa, l2, dv, x, total;
+};
+__host__ __device__ constexpr Layout layout(int Sp) {
+    return Layout{0,
+                  Sp * RP,
+                  2 * Sp * RP,
+                  2 * Sp * RP + Sp * D,
+                  2 * Sp * RP + Sp * D + Sp,
+                  2 * Sp * RP + Sp * D + 2 * Sp,
+                  2 * Sp * RP + Sp * D + 2 * Sp + NW * BK * XP};
+}
+constexpr int kMaxLdsBytes = layout(MAXS).total * 4;
+
+// Wait until *flag >= v (another wave of the workgroup stores it with
+// release order), for at most kSpinMax polls.
+__device__ __forceinline__ void wait_ge(const int* flag, int v) {
+    for (int n = 0; n < kSpinMax; ++n) {
+        if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+__device__ __forceinline__ void set_flag(int* flag, int v) {
+    __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Key of dQ product step s in lane half h (any bijection of the 32 keys
+// works; this one puts the two halves' scratch rows 8 apart, on disjoint
+// LDS banks).
+__device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 * h + (s & 7); }
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ int simd_slots[NW];
+    __shared__ int staged[NW];  // query tile t's rows are in LDS
+    __shared__ int chain[NW];   // contributions summed into query tile t's dQ partial
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, hf = lane >> 5;
+    const int bhi = blockIdx.x;
+    const int b = bhi / a.H, h = bhi % a.H;
+    const int S = a.S, nt = (S + BK - 1) / BK, Sp = nt * BK;
+    const Layout L = layout(Sp);
+    float* const Qr = lds + L.q;
+    float* const Gr = lds + L.g;
+    float* const DQA = lds + L.dqa;  // dQ partials; row q kept at row q ^ ((q >> 2) & 1)
+    float* const L2 = lds + L.l2;
+    float* const DV = lds + L.dv;
+    float* const X = lds + L.x + wave * BK * XP;
+    const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
+
+    if (tid < NW) staged[tid] = chain[tid] = 0;
+    // Key tile of this wave: SIMD s (ranks 2s, 2s+1) takes tiles s and
+    // nt-1-s, so causal work pairs up to nt + 1 tiles per SIMD.  The rank's
+    // barrier also publishes the cleared flags.
+    const int sr = fa::simd_rank<NW>(simd_slots, wave, lane);
+    const int s2 = sr >> 1;
+    int kt = -1;
+    if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
+    if (kt < 0) return;
+
+    // Stage query tile kt: Q and dO rows, Dq = dO . O, lse' = lse log2 e
+    // (+inf past S: P = 0 there).  Rows past S load as zero.
+    {
+        RowLoader ql, gl, ol;
+        ql.init(a.q + base, a.ts, S, D);
+        gl.init(a.go + base, a.ts, S, D);
+        ol.init(a.o + base, a.ts, S, D);
+#pragma unroll
+        for (int k = 0; k < BK * CPR / 64; ++k) {
+            const int f = lane + 64 * k;
+            const int row = kt * BK + f / CPR, cc = f % CPR;
+            const floatx4 qv = ql.load(row, cc), gv = gl.load(row, cc), ov = ol.load(row, cc);
+            *reinterpret_cast<floatx4*>(Qr + row * RP + 4 * cc) = qv;
+            *reinterpret_cast<floatx4*>(Gr + row * RP + 4 * cc) = gv;
+            float d = gv[0] * ov[0];
+#pragma unroll
+            for (int j = 1; j < 4; ++j) d = fmaf(gv[j], ov[j], d);
+#pragma unroll
+            for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
+            if (cc == 0) DV[row] = d;
+        }
+        if (lane < BK) {
+            const int q = kt * BK + lane;
+            L2[q] = q < S ? a.lse[(int64_t)bhi * S + q] * kLog2e : kInf;
+        }
+    }
+
+    const int kj = kt * BK + c;
+    const bool kval = kj < S;
+    // K pre-scaled to log2 units and V (B operands of S' and dP, lane (c, h)
+    // holds dims 16h .. 16h+15 of key kj), and K as the B operand of dQ
+    // (step s: key dq_key(s, h), dim c), read back through the scratch
+    float kr2[D / 2], vr[D / 2], kq[16];
+    {
+        const float qsc = a.scale * kLog2e;
+        const float* kp = a.k + base + (int64_t)kj * a.ts + hf * (D / 2);
+        const float* vp = a.v + base + (int64_t)kj * a.ts + hf * (D / 2);
+#pragma unroll
+        for (int s = 0; s < D / 2; s += 4) {
+            const floatx4 kv = kval ? *reinterpret_cast<const floatx4*>(kp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+            const floatx4 vv = kval ? *reinterpret_cast<const floatx4*>(vp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + s) = kv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                kr2[s + j] = kv[j] * qsc;
+                vr[s + j] = vv[j];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) kq[s] = X[dq_key(s, hf) * XP + c];
+    }
+    set_flag(&staged[kt], 1);
+
+    floatx16 accv, acck;  // dV^T, dK^T (unscaled): register r <-> dim acc_key(r, h), lane <-> key
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accv[r] = acck[r] = 0.f;
+
+    const bool kedge = kt * BK + BK > S;  // keys past S in this tile
+    const int nsteps = CAUSAL ? nt - kt : nt;
+    for (int t = 0; t < nsteps; ++t) {
+        int i = kt + t;
+        if (!CAUSAL && i >= nt) i -= nt;
+        if (t > 0) wait_ge(&staged[i], 1);
+        const float* qt = Qr + i * BK * RP;
+        const float* gt = Gr + i * BK * RP;
+        floatx16 sc, dp;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
+        Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S', register r <-> query i*32 + acc_key(r, h)
+        Tiles<D>::dchain(dp, gt, vr, c, hf);   // dP
+        const bool edge = kedge || (CAUSAL && t == 0);
+        floatx16 p, ds;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
+            const floatx4 d4 = *reinterpret_cast<const floatx4*>(DV + i * BK + 8 * g + 4 * hf);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = 4 * g + j;
+                float pv = fast_exp2(sc[r] - l4[j]);
+                if (edge && !(kval && (!CAUSAL || kj <= i * BK + acc_key(r, hf)))) pv = 0.f;
+                p[r] = pv;
+                ds[r] = pv * (dp[r] - d4[j]);
+            }
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS: A[d][query] read from the row-major tiles
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int q = acc_key(r, hf);
+            accv = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[q * RP + c], p[r], accv, 0, 0, 0);
+            acck = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[q * RP + c], ds[r], acck, 0, 0, 0);
+        }
+        // dQ tile = dS K: dS^T through the scratch ([key][query]), then
+        // A[query][key] = X[key][query]
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
+                floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
+        floatx16 aq;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) aq[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
+        // Chain: register r <-> query i*32 + acc_key(r, h), lane <-> dim c.
+        // The two halves' rows (4 apart) sit on opposite parities: disjoint banks.
+        const int nc = CAUSAL ? i + 1 : nt;  // contributors of tile i
+        float* const part = DQA + i * BK * D;
+        if (t > 0) {
+            wait_ge(&chain[i], t);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) aq[r] += part[(acc_key(r, hf) ^ hf) * D + c];
+        }
+        if (t == nc - 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int q = i * BK + acc_key(r, hf);
+                if (q < S) a.dq[base + (int64_t)q * a.ts + c] = a.scale * aq[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[(acc_key(r, hf) ^ hf) * D + c] = aq[r];
+            set_flag(&chain[i], t + 1);
+        }
+    }
+    if (kval) {
+        float* dvp = a.dv + base + (int64_t)kj * a.ts;
+        float* dkp = a.dk + base + (int64_t)kj * a.ts;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 8 * g + 4 * hf;
+            *reinterpret_cast<floatx4*>(dvp + d0) = floatx4{accv[4 * g], accv[4 * g + 1], accv[4 * g + 2], accv[4 * g + 3]};
+            *reinterpret_cast<floatx4*>(dkp + d0) = floatx4{a.scale * acck[4 * g], a.scale * acck[4 * g + 1],
+                                                            a.scale * acck[4 * g + 2], a.scale * acck[4 * g + 3]};
+        }
+    }
+}
+
+}  // namespace bh
+
+// Recompute mode with D = 32, S <= 256 and the tiled kernels' layout
+// conditions (bwd_tiled_ok).
+inline bool bh_ok(const BwdArgs& a) { return !a.probs && a.D == bh::D && a.S >= 1 && a.S <= bh::MAXS; }
+
+template <bool CAUSAL>
+hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
+    const int64_t grid = (int64_t)a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    auto kern = bh::bwd_bh_kernel<CAUSAL>;
+    // The dynamic-LDS limit is raised once per device (bit d of attr_set).
+    static std::atomic<unsigned long long> attr_set{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const unsigned long long bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
+    if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                bh::kMaxLdsBytes);
+        if (e != hipSuccess) return e;
+        attr_set.fetch_or(bit, std::memory_order_release);
+    }
+    const int Sp = (a.S + BK - 1) / BK * BK;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bh::NW * 64), (size_t)bh::layout(Sp).total * 4, s, a);
+    return hipGetLastError();
+}
+
+inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
+    return a.causal ? launch_bh_mode<true>(a, s) : launch_bh_mode<false>(a, s);
+}
+
+}  // namespace bwd
+}  // namespace hipgpt

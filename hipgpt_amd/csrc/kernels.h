@@ -50,7 +50,8 @@ struct BwdArgs {
     float *dq, *dk, *dv, *dvec;
     // Recompute mode (probs == nullptr): the forward's output O and row
     // log-sum-exp lse [B*H][S] (natural log); P is rebuilt per tile as
-    // exp(scale q.k - lse) and dvec receives the row dots dO . O.
+    // exp(scale q.k - lse) and the row dots dO . O are formed from dO and O
+    // (dvec is unused).
     const float *o, *lse;
     int64_t bs, ts, hs;
     int B, H, S, D;

@@ -77,7 +77,6 @@ def test_strerror_and_host_validation():
     assert fl(p + 4, p, p, 1, 8, 64, 2, 1, None) == _lib.ERR_UNSUPPORTED  # qkv not 16-byte aligned
     assert bl(p, p, None, p, p, 1, 8, 64, 2, 1, p, 1 << 20, None) == _lib.ERR_INVALID
     assert bl(p, p, p, None, p, 1, 8, 64, 2, 1, p, 1 << 20, None) == _lib.ERR_INVALID
-    assert bl(p, p, p, p, p, 1, 8, 64, 2, 1, None, 0, None) == _lib.ERR_WORKSPACE
     assert bl(p, p, p, p, p, 1, 8, 256, 2, 1, p, 1 << 20, None) == _lib.ERR_UNSUPPORTED  # D = 128
     # KV-cache decode: null lens / caches, bad sizes, unsupported D, missing workspace
     kvc = L.hipgpt_attn_decode_kvcache
