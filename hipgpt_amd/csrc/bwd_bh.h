@@ -27,12 +27,13 @@
 // rows, lse', Dq = dO . O) and flags it, so no workgroup-wide barrier follows
 // the start.  The summation order is fixed: results are deterministic.
 //
-// One launch, no atomics, no workspace; the LDS footprint (145 KB at
+// One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
 // key tiles j and nt-1-j share a SIMD (nt + 1 tiles per SIMD).
 #pragma once
 
 #include <atomic>
+#include <type_traits>
 
 #include "bwd_tiled.h"
 #include "common.h"
@@ -48,6 +49,7 @@ constexpr int NW = 8;          // waves; at most one key tile each
 constexpr int MAXS = NW * BK;  // longest sequence
 constexpr int RP = D + 4;      // pitch of the Q / dO rows
 constexpr int XP = BK + 4;     // pitch of a wave's dS^T scratch ([key][query])
+constexpr int PP = D + 8;      // pitch of the dQ partials: rows q and q+4 on disjoint banks
 constexpr int CPR = D / 4;     // 16-byte chunks per row
 
 constexpr int kSpinMax = 1 << 20;  // bound of a flag wait (~0.1 s)
@@ -60,10 +62,10 @@ __host__ __device__ constexpr Layout layout(int Sp) {
     return Layout{0,
                   Sp * RP,
                   2 * Sp * RP,
-                  2 * Sp * RP + Sp * D,
-                  2 * Sp * RP + Sp * D + Sp,
-                  2 * Sp * RP + Sp * D + 2 * Sp,
-                  2 * Sp * RP + Sp * D + 2 * Sp + NW * BK * XP};
+                  2 * Sp * RP + Sp * PP,
+                  2 * Sp * RP + Sp * PP + Sp,
+                  2 * Sp * RP + Sp * PP + 2 * Sp,
+                  2 * Sp * RP + Sp * PP + 2 * Sp + NW * BK * XP};
 }
 constexpr int kMaxLdsBytes = layout(MAXS).total * 4;
 
@@ -99,7 +101,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const Layout L = layout(Sp);
     float* const Qr = lds + L.q;
     float* const Gr = lds + L.g;
-    float* const DQA = lds + L.dqa;  // dQ partials; row q kept at row q ^ ((q >> 2) & 1)
+    float* const DQA = lds + L.dqa;  // dQ partials [Sp][PP]
     float* const L2 = lds + L.l2;
     float* const DV = lds + L.dv;
     float* const X = lds + L.x + wave * BK * XP;
@@ -174,30 +176,87 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 
     const bool kedge = kt * BK + BK > S;  // keys past S in this tile
     const int nsteps = CAUSAL ? nt - kt : nt;
-    for (int t = 0; t < nsteps; ++t) {
+    // dQ term of the job whose dS^T is in the scratch: A[query][key] = X[key][query]
+    auto dq_term = [&]() {
+        floatx16 aq;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) aq[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+            aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
+        return aq;
+    };
+    // dQ rows through a buffer resource ending at row S-1: stores past it are
+    // dropped, and each register's row offset is a scalar.
+    const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(
+        a.dq + base, 0, (int)(((int64_t)(S - 1) * a.ts + D) * 4), kBufferFlags);
+    const int row4 = a.ts * 4;
+    // Chain step t of query tile i: register r <-> query i*32 + acc_key(r, h),
+    // lane <-> dim c.
+    auto chain_add = [&](floatx16 aq, int i, int t) {
+        const int nc = CAUSAL ? i + 1 : nt;  // contributors of tile i
+        float* const part = DQA + (i * BK + 4 * hf) * PP + c;
+        if (t > 0) {
+            wait_ge(&chain[i], t);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) aq[r] += part[(8 * (r >> 2) + (r & 3)) * PP];
+        }
+        if (t == nc - 1) {
+            const int vo = (i * BK + 4 * hf) * row4 + c * 4;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr, vo,
+                                                      (8 * (r >> 2) + (r & 3)) * row4, 0);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = aq[r];
+            set_flag(&chain[i], t + 1);
+        }
+    };
+    // Job t (query tile i).  The previous job's dQ term is formed alongside
+    // this job's S' and dP products (one basic block, so their MFMAs and LDS
+    // reads interleave) and enters the chain after this job's dV / dK.
+    int iprev = 0;
+    auto job = [&](auto has_prev, int t) {
+        constexpr bool HP = decltype(has_prev)::value;
         int i = kt + t;
         if (!CAUSAL && i >= nt) i -= nt;
-        if (t > 0) wait_ge(&staged[i], 1);
+        if (HP) wait_ge(&staged[i], 1);
         const float* qt = Qr + i * BK * RP;
         const float* gt = Gr + i * BK * RP;
+        // The chains start from -lse' and -Dq, so they end at S' - lse' and
+        // dP - Dq: P = exp2(first), dS = P * second.
         floatx16 sc, dp;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[r] = dp[r] = 0.f;
-        Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S', register r <-> query i*32 + acc_key(r, h)
-        Tiles<D>::dchain(dp, gt, vr, c, hf);   // dP
-        const bool edge = kedge || (CAUSAL && t == 0);
-        floatx16 p, ds;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const floatx4 l4 = *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
             const floatx4 d4 = *reinterpret_cast<const floatx4*>(DV + i * BK + 8 * g + 4 * hf);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = 4 * g + j;
-                float pv = fast_exp2(sc[r] - l4[j]);
-                if (edge && !(kval && (!CAUSAL || kj <= i * BK + acc_key(r, hf)))) pv = 0.f;
-                p[r] = pv;
-                ds[r] = pv * (dp[r] - d4[j]);
+                sc[4 * g + j] = -l4[j];
+                dp[4 * g + j] = -d4[j];
+            }
+        }
+        Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S' - lse', register r <-> query i*32 + acc_key(r, h)
+        Tiles<D>::dchain(dp, gt, vr, c, hf);   // dP - Dq
+        floatx16 aq;
+        if constexpr (HP) aq = dq_term();
+        // masks: keys past S (last key tile) and, causally, keys past the
+        // query on the diagonal job (t == 0)
+        const bool edge = HP ? kedge : (kedge || CAUSAL);
+        floatx16 p, ds;
+        if (edge) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const bool vis = kval && (!CAUSAL || kj <= i * BK + acc_key(r, hf));
+                p[r] = vis ? fast_exp2(sc[r]) : 0.f;
+                ds[r] = p[r] * dp[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                p[r] = fast_exp2(sc[r]);
+                ds[r] = p[r] * dp[r];
             }
         }
         // dV^T += dO^T P, dK^T += Q^T dS: A[d][query] read from the row-major tiles
@@ -207,39 +266,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             accv = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[q * RP + c], p[r], accv, 0, 0, 0);
             acck = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[q * RP + c], ds[r], acck, 0, 0, 0);
         }
-        // dQ tile = dS K: dS^T through the scratch ([key][query]), then
-        // A[query][key] = X[key][query]
+        if constexpr (HP) chain_add(aq, iprev, t - 1);
+        // this job's dS^T into the scratch ([key][query]; the previous job's
+        // reads of it were issued above, and a wave's LDS accesses run in order)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
             *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
                 floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
-        floatx16 aq;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) aq[r] = 0.f;
-#pragma unroll
-        for (int s = 0; s < 16; ++s)
-            aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
-        // Chain: register r <-> query i*32 + acc_key(r, h), lane <-> dim c.
-        // The two halves' rows (4 apart) sit on opposite parities: disjoint banks.
-        const int nc = CAUSAL ? i + 1 : nt;  // contributors of tile i
-        float* const part = DQA + i * BK * D;
-        if (t > 0) {
-            wait_ge(&chain[i], t);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) aq[r] += part[(acc_key(r, hf) ^ hf) * D + c];
-        }
-        if (t == nc - 1) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int q = i * BK + acc_key(r, hf);
-                if (q < S) a.dq[base + (int64_t)q * a.ts + c] = a.scale * aq[r];
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) part[(acc_key(r, hf) ^ hf) * D + c] = aq[r];
-            set_flag(&chain[i], t + 1);
-        }
-    }
+        iprev = i;
+    };
+    job(std::false_type{}, 0);
+    for (int t = 1; t < nsteps; ++t) job(std::true_type{}, t);
+    chain_add(dq_term(), iprev, nsteps - 1);
+
     if (kval) {
         float* dvp = a.dv + base + (int64_t)kj * a.ts;
         float* dkp = a.dk + base + (int64_t)kj * a.ts;
