@@ -54,6 +54,11 @@ constexpr int CPR = D / 4;     // 16-byte chunks per row
 
 constexpr int kSpinMax = 1 << 20;  // bound of a flag wait (~0.1 s)
 
+// HBM bytes per s_memrealtime tick (10 ns) assumed by the staggered start.
+#ifndef HIPGPT_BH_SLOT_DIV
+#define HIPGPT_BH_SLOT_DIV 60000
+#endif
+
 // LDS layout in floats for Sp = S rounded up to 32 rows.
 struct Layout {
     int q, g, dqa, l2, dv, x, total;
@@ -88,6 +93,7 @@ __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 *
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
+    const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ int simd_slots[NW];
     __shared__ int staged[NW];  // query tile t's rows are in LDS
@@ -116,6 +122,20 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     int kt = -1;
     if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
     if (kt < 0) return;
+
+    // Causal: key tile kt first needs query tile kt + t at its step t, and the
+    // wave of key tile 0 has the most steps.  Starting wave kt's loads kt
+    // slots after the workgroup start (a slot: the time HBM takes to deliver
+    // one key tile's rows for every resident workgroup, at ~6 TB/s) lets the
+    // early key tiles' rows arrive first instead of every wave waiting for all
+    // of them.  s_memrealtime counts 10 ns; the wait is at most 7 slots.
+    if (CAUSAL && kt > 0) {
+        constexpr int kWaveBytes = 5 * BK * D * 4;  // Q, dO, O rows + K, V rows
+        const int resident = gridDim.x < 256u ? (int)gridDim.x : 256;
+        const unsigned long long slot = (unsigned long long)resident * kWaveBytes / HIPGPT_BH_SLOT_DIV;
+        const unsigned long long until = t_start + slot * kt;
+        for (int n = 0; n < 4096 && __builtin_amdgcn_s_memrealtime() < until; ++n) __builtin_amdgcn_s_sleep(2);
+    }
 
     // Stage query tile kt: Q and dO rows, Dq = dO . O, lse' = lse log2 e
     // (+inf past S: P = 0 there).  Rows past S load as zero.
