@@ -138,51 +138,60 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     }
 
     // Stage query tile kt: Q and dO rows, Dq = dO . O, lse' = lse log2 e
-    // (+inf past S: P = 0 there).  Rows past S load as zero.
+    // (+inf past S: P = 0 there); and the wave's keys: K pre-scaled to log2
+    // units and V (B operands of S' and dP, lane (c, h) holds dims
+    // 16h .. 16h+15 of key kj), and K as the B operand of dQ (step s: key
+    // dq_key(s, h), dim c), read back through the scratch.  Every global load
+    // is issued before the first use (one round trip); rows past S load as zero.
+    const int kj = kt * BK + c;
+    const bool kval = kj < S;
+    float kr2[D / 2], vr[D / 2], kq[16];
     {
-        RowLoader ql, gl, ol;
+        RowLoader ql, gl, ol, kl, vl;
         ql.init(a.q + base, a.ts, S, D);
         gl.init(a.go + base, a.ts, S, D);
         ol.init(a.o + base, a.ts, S, D);
+        kl.init(a.k + base, a.ts, S, D);
+        vl.init(a.v + base, a.ts, S, D);
+        constexpr int NK = BK * CPR / 64;
+        floatx4 qv[NK], gv[NK], ov[NK], kv[D / 8], vv[D / 8];
 #pragma unroll
-        for (int k = 0; k < BK * CPR / 64; ++k) {
+        for (int k = 0; k < NK; ++k) {
             const int f = lane + 64 * k;
             const int row = kt * BK + f / CPR, cc = f % CPR;
-            const floatx4 qv = ql.load(row, cc), gv = gl.load(row, cc), ov = ol.load(row, cc);
-            *reinterpret_cast<floatx4*>(Qr + row * RP + 4 * cc) = qv;
-            *reinterpret_cast<floatx4*>(Gr + row * RP + 4 * cc) = gv;
-            float d = gv[0] * ov[0];
+            qv[k] = ql.load(row, cc);
+            gv[k] = gl.load(row, cc);
+            ov[k] = ol.load(row, cc);
+        }
 #pragma unroll
-            for (int j = 1; j < 4; ++j) d = fmaf(gv[j], ov[j], d);
+        for (int s = 0; s < D / 8; ++s) {
+            kv[s] = kl.load(kj, hf * (D / 8) + s);
+            vv[s] = vl.load(kj, hf * (D / 8) + s);
+        }
+        const int ql2 = kt * BK + (lane & (BK - 1));
+        const float lsev = ql2 < S ? a.lse[(int64_t)bhi * S + ql2] : 0.f;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int f = lane + 64 * k;
+            const int row = kt * BK + f / CPR, cc = f % CPR;
+            *reinterpret_cast<floatx4*>(Qr + row * RP + 4 * cc) = qv[k];
+            *reinterpret_cast<floatx4*>(Gr + row * RP + 4 * cc) = gv[k];
+            float d = gv[k][0] * ov[k][0];
+#pragma unroll
+            for (int j = 1; j < 4; ++j) d = fmaf(gv[k][j], ov[k][j], d);
 #pragma unroll
             for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
             if (cc == 0) DV[row] = d;
         }
-        if (lane < BK) {
-            const int q = kt * BK + lane;
-            L2[q] = q < S ? a.lse[(int64_t)bhi * S + q] * kLog2e : kInf;
-        }
-    }
-
-    const int kj = kt * BK + c;
-    const bool kval = kj < S;
-    // K pre-scaled to log2 units and V (B operands of S' and dP, lane (c, h)
-    // holds dims 16h .. 16h+15 of key kj), and K as the B operand of dQ
-    // (step s: key dq_key(s, h), dim c), read back through the scratch
-    float kr2[D / 2], vr[D / 2], kq[16];
-    {
+        if (lane < BK) L2[ql2] = ql2 < S ? lsev * kLog2e : kInf;
         const float qsc = a.scale * kLog2e;
-        const float* kp = a.k + base + (int64_t)kj * a.ts + hf * (D / 2);
-        const float* vp = a.v + base + (int64_t)kj * a.ts + hf * (D / 2);
 #pragma unroll
-        for (int s = 0; s < D / 2; s += 4) {
-            const floatx4 kv = kval ? *reinterpret_cast<const floatx4*>(kp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
-            const floatx4 vv = kval ? *reinterpret_cast<const floatx4*>(vp + s) : floatx4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + s) = kv;
+        for (int s = 0; s < D / 8; ++s) {
+            *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = kv[s];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                kr2[s + j] = kv[j] * qsc;
-                vr[s + j] = vv[j];
+                kr2[4 * s + j] = kv[s][j] * qsc;
+                vr[4 * s + j] = vv[s][j];
             }
         }
 #pragma unroll
