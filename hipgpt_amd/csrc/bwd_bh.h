@@ -1,6 +1,8 @@
-// bwd_bh.h -- probs-free attention backward with one workgroup per (b, h),
-// for head dim 32 and S <= 256: the shape of HipGPT's default model
+// bwd_bh.h -- attention backward with one workgroup per (b, h), for head
+// dim 32 and S <= 256: the shape of HipGPT's default model
 // (src/train_gpt.cpp:175-180), whose backward is src/hip_kernels.cpp:1159-1272.
+// Two modes: probs-free (P rebuilt from the forward's O and row lse) and the
+// reference's contract (P read from the stored probs; see PROBS below).
 //
 // One (b, h) problem fits one CU: Q and dO rows, the row log-sum-exp and
 // Dq = dO . O stay in LDS for the whole launch, and each of the 8 waves keeps
@@ -26,6 +28,14 @@
 // bounded besides.  Each wave stages its own diagonal query tile (Q, dO
 // rows, lse', Dq = dO . O) and flags it, so no workgroup-wide barrier follows
 // the start.  The summation order is fixed: results are deterministic.
+//
+// PROBS (the stored [S][S] probs instead of O and lse): P is read from
+// memory instead of rebuilt, and Dq = sum_j P_ij dP_ij = dO_i . (P V)_i needs
+// O = P V first.  Phase 1 forms it along the same chain (each key tile adds
+// its P V term, 16 MFMAs per job, the finished rows staying in LDS); after a
+// workgroup barrier every thread forms Dq for its rows, and after a second
+// barrier phase 2 runs the jobs above with the loaded P.  80 MFMAs per job as
+// in the probs-free mode; P is read twice (once per phase).
 //
 // One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
@@ -91,13 +101,14 @@ __device__ __forceinline__ void set_flag(int* flag, int v) {
 // LDS banks).
 __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 * h + (s & 7); }
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool PROBS>
 __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ int simd_slots[NW];
     __shared__ int staged[NW];  // query tile t's rows are in LDS
     __shared__ int chain[NW];   // contributions summed into query tile t's dQ partial
+    __shared__ int ochain[NW];  // stored probs: contributions summed into query tile t's O partial
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, hf = lane >> 5;
@@ -113,7 +124,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     float* const X = lds + L.x + wave * BK * XP;
     const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
 
-    if (tid < NW) staged[tid] = chain[tid] = 0;
+    if (tid < NW) staged[tid] = chain[tid] = ochain[tid] = 0;
     // Key tile of this wave: SIMD s (ranks 2s, 2s+1) takes tiles s and
     // nt-1-s, so causal work pairs up to nt + 1 tiles per SIMD.  The rank's
     // barrier also publishes the cleared flags.
@@ -121,7 +132,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const int s2 = sr >> 1;
     int kt = -1;
     if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
-    if (kt < 0) return;
+    // (stored probs: idle waves stay for the workgroup barriers below)
+    if (!PROBS && kt < 0) return;
+    const bool active = kt >= 0;
 
     // Causal: key tile kt first needs query tile kt + t at its step t, and the
     // wave of key tile 0 has the most steps.  Starting wave kt's loads kt
@@ -129,7 +142,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // one key tile's rows for every resident workgroup, at ~6 TB/s) lets the
     // early key tiles' rows arrive first instead of every wave waiting for all
     // of them.  s_memrealtime counts 10 ns; the wait is at most 7 slots.
-    if (CAUSAL && kt > 0) {
+    if (!PROBS && CAUSAL && kt > 0) {
         constexpr int kWaveBytes = 5 * BK * D * 4;  // Q, dO, O rows + K, V rows
         const int resident = gridDim.x < 256u ? (int)gridDim.x : 256;
         const unsigned long long slot = (unsigned long long)resident * kWaveBytes / HIPGPT_BH_SLOT_DIV;
@@ -137,20 +150,21 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         for (int n = 0; n < 4096 && __builtin_amdgcn_s_memrealtime() < until; ++n) __builtin_amdgcn_s_sleep(2);
     }
 
-    // Stage query tile kt: Q and dO rows, Dq = dO . O, lse' = lse log2 e
-    // (+inf past S: P = 0 there); and the wave's keys: K pre-scaled to log2
-    // units and V (B operands of S' and dP, lane (c, h) holds dims
-    // 16h .. 16h+15 of key kj), and K as the B operand of dQ (step s: key
-    // dq_key(s, h), dim c), read back through the scratch.  Every global load
-    // is issued before the first use (one round trip); rows past S load as zero.
+    // Stage query tile kt: Q and dO rows, and (recompute) Dq = dO . O and
+    // lse' = lse log2 e (+inf past S: P = 0 there); and the wave's keys: K
+    // pre-scaled to log2 units and V (B operands of S' and dP, lane (c, h)
+    // holds dims 16h .. 16h+15 of key kj), K (and, stored probs, V) as the B
+    // operand of a product over keys (step s: key dq_key(s, h), dim c), read
+    // back through the scratch.  Every global load is issued before the
+    // first use (one round trip); rows past S load as zero.
     const int kj = kt * BK + c;
-    const bool kval = kj < S;
-    float kr2[D / 2], vr[D / 2], kq[16];
-    {
+    const bool kval = active && kj < S;
+    float kr2[D / 2], vr[D / 2], kq[16], vq[PROBS ? 16 : 1];
+    if (active) {
         RowLoader ql, gl, ol, kl, vl;
         ql.init(a.q + base, a.ts, S, D);
         gl.init(a.go + base, a.ts, S, D);
-        ol.init(a.o + base, a.ts, S, D);
+        if (!PROBS) ol.init(a.o + base, a.ts, S, D);
         kl.init(a.k + base, a.ts, S, D);
         vl.init(a.v + base, a.ts, S, D);
         constexpr int NK = BK * CPR / 64;
@@ -161,7 +175,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             const int row = kt * BK + f / CPR, cc = f % CPR;
             qv[k] = ql.load(row, cc);
             gv[k] = gl.load(row, cc);
-            ov[k] = ol.load(row, cc);
+            if (!PROBS) ov[k] = ol.load(row, cc);
         }
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) {
@@ -169,21 +183,23 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             vv[s] = vl.load(kj, hf * (D / 8) + s);
         }
         const int ql2 = kt * BK + (lane & (BK - 1));
-        const float lsev = ql2 < S ? a.lse[(int64_t)bhi * S + ql2] : 0.f;
+        const float lsev = (!PROBS && ql2 < S) ? a.lse[(int64_t)bhi * S + ql2] : 0.f;
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
             const int f = lane + 64 * k;
             const int row = kt * BK + f / CPR, cc = f % CPR;
             *reinterpret_cast<floatx4*>(Qr + row * RP + 4 * cc) = qv[k];
             *reinterpret_cast<floatx4*>(Gr + row * RP + 4 * cc) = gv[k];
-            float d = gv[k][0] * ov[k][0];
+            if constexpr (!PROBS) {
+                float d = gv[k][0] * ov[k][0];
 #pragma unroll
-            for (int j = 1; j < 4; ++j) d = fmaf(gv[k][j], ov[k][j], d);
+                for (int j = 1; j < 4; ++j) d = fmaf(gv[k][j], ov[k][j], d);
 #pragma unroll
-            for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
-            if (cc == 0) DV[row] = d;
+                for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
+                if (cc == 0) DV[row] = d;
+            }
         }
-        if (lane < BK) L2[ql2] = ql2 < S ? lsev * kLog2e : kInf;
+        if (!PROBS && lane < BK) L2[ql2] = ql2 < S ? lsev * kLog2e : kInf;
         const float qsc = a.scale * kLog2e;
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) {
@@ -196,15 +212,101 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s) kq[s] = X[dq_key(s, hf) * XP + c];
+        if constexpr (PROBS) {
+            // V the same way, after the K reads (a wave's LDS accesses run in order)
+#pragma unroll
+            for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = vv[s];
+#pragma unroll
+            for (int s = 0; s < 16; ++s) vq[s] = X[dq_key(s, hf) * XP + c];
+        }
     }
-    set_flag(&staged[kt], 1);
+    if (!PROBS) set_flag(&staged[kt], 1);
+
+    const bool kedge = kt * BK + BK > S;  // keys past S in this tile
+    const int nsteps = CAUSAL ? nt - kt : nt;
+    // the (b, h) slice of the stored probs [S][S] through a buffer resource:
+    // rows past S read as zero
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        PROBS ? const_cast<float*>(a.probs) + (int64_t)bhi * S * S : nullptr, 0, PROBS ? S * S * 4 : 0, kBufferFlags);
+    const int S4 = S * 4;
+
+    if constexpr (PROBS) {
+        // Phase 1: O = P V summed over key tiles along the same chain as dQ
+        // (step t: query tile kt + t), the last contributor leaving the
+        // finished rows in the partial buffer; then Dq = dO . O per row.
+        if (active) {
+            // P[query i*32 + c][key kt*32 + dq_key(s, h)] for s = 8u + 4w + j;
+            // the next job's tile is requested before this one's products
+            auto load_pa = [&](floatx4 (&pa)[4], int i) {
+                const int vo = (i * BK + c) * S4 + (kt * BK + 8 * hf) * 4;
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int w = 0; w < 2; ++w) {
+                        const floatx4 v = __builtin_bit_cast(
+                            floatx4, __builtin_amdgcn_raw_buffer_load_b128(pr, vo + (16 * u + 4 * w) * 4, 0, 0));
+                        pa[2 * u + w] = (kt * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                    }
+            };
+            floatx4 pn[4];
+            load_pa(pn, kt);
+            for (int t = 0; t < nsteps; ++t) {
+                int i = kt + t;
+                if (!CAUSAL && i >= nt) i -= nt;
+                floatx4 pa[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) pa[k] = pn[k];
+                if (t + 1 < nsteps) load_pa(pn, i + 1 < nt ? i + 1 : 0);
+                floatx16 o;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < 16; ++s) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[s >> 2][s & 3], vq[s], o, 0, 0, 0);
+                const int nc = CAUSAL ? i + 1 : nt;
+                float* const part = DQA + (i * BK + 4 * hf) * PP + c;
+                if (t > 0) {
+                    wait_ge(&ochain[i], t);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[r] += part[(8 * (r >> 2) + (r & 3)) * PP];
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = o[r];
+                if (t < nc - 1) set_flag(&ochain[i], t + 1);
+            }
+        }
+        __syncthreads();
+        // Sp * CPR is a multiple of 256: a wave's lanes are all in or all out
+        for (int f = tid; f < Sp * CPR; f += NW * 64) {
+            const int row = f / CPR, cc = f % CPR;
+            const floatx4 o4 = *reinterpret_cast<const floatx4*>(DQA + row * PP + 4 * cc);
+            const floatx4 g4 = *reinterpret_cast<const floatx4*>(Gr + row * RP + 4 * cc);
+            float d = g4[0] * o4[0];
+#pragma unroll
+            for (int j = 1; j < 4; ++j) d = fmaf(g4[j], o4[j], d);
+#pragma unroll
+            for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
+            if (cc == 0) DV[row] = d;
+        }
+        __syncthreads();
+        if (!active) return;
+    }
+
+    // Stored probs, phase 2: P of query tile i in the accumulator's order
+    // (register r <-> query i*32 + acc_key(r, h), lane <-> key kj); keys
+    // past S read as zero through an out-of-range offset.
+    auto load_pk = [&](floatx16& pv, int i) {
+        const int vo = kval ? (i * BK + 4 * hf) * S4 + kj * 4 : 0x40000000;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            pv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, vo, (8 * (r >> 2) + (r & 3)) * S4, 0));
+    };
+    floatx16 pnext;
+    if constexpr (PROBS) load_pk(pnext, kt);
 
     floatx16 accv, acck;  // dV^T, dK^T (unscaled): register r <-> dim acc_key(r, h), lane <-> key
 #pragma unroll
     for (int r = 0; r < 16; ++r) accv[r] = acck[r] = 0.f;
 
-    const bool kedge = kt * BK + BK > S;  // keys past S in this tile
-    const int nsteps = CAUSAL ? nt - kt : nt;
     // dQ term of the job whose dS^T is in the scratch: A[query][key] = X[key][query]
     auto dq_term = [&]() {
         floatx16 aq;
@@ -250,7 +352,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         constexpr bool HP = decltype(has_prev)::value;
         int i = kt + t;
         if (!CAUSAL && i >= nt) i -= nt;
-        if (HP) wait_ge(&staged[i], 1);
+        if (HP && !PROBS) wait_ge(&staged[i], 1);  // stored probs: staged before the barriers
         const float* qt = Qr + i * BK * RP;
         const float* gt = Gr + i * BK * RP;
         // The chains start from -lse' and -Dq, so they end at S' - lse' and
@@ -258,7 +360,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         floatx16 sc, dp;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const floatx4 l4 = *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
+            const floatx4 l4 = PROBS ? floatx4{0.f, 0.f, 0.f, 0.f}
+                                     : *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
             const floatx4 d4 = *reinterpret_cast<const floatx4*>(DV + i * BK + 8 * g + 4 * hf);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -266,15 +369,24 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
                 dp[4 * g + j] = -d4[j];
             }
         }
-        Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S' - lse', register r <-> query i*32 + acc_key(r, h)
-        Tiles<D>::dchain(dp, gt, vr, c, hf);   // dP - Dq
+        floatx16 p, ds;
+        if constexpr (PROBS) {
+            // stored probs (a causal forward wrote zeros above the diagonal)
+            p = pnext;
+            if (t + 1 < nsteps) load_pk(pnext, i + 1 < nt ? i + 1 : 0);
+        } else {
+            Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S' - lse', register r <-> query i*32 + acc_key(r, h)
+        }
+        Tiles<D>::dchain(dp, gt, vr, c, hf);  // dP - Dq
         floatx16 aq;
         if constexpr (HP) aq = dq_term();
         // masks: keys past S (last key tile) and, causally, keys past the
         // query on the diagonal job (t == 0)
         const bool edge = HP ? kedge : (kedge || CAUSAL);
-        floatx16 p, ds;
-        if (edge) {
+        if constexpr (PROBS) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
+        } else if (edge) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const bool vis = kval && (!CAUSAL || kj <= i * BK + acc_key(r, hf));
@@ -323,15 +435,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 
 }  // namespace bh
 
-// Recompute mode with D = 32, S <= 256 and the tiled kernels' layout
-// conditions (bwd_tiled_ok).
-inline bool bh_ok(const BwdArgs& a) { return !a.probs && a.D == bh::D && a.S >= 1 && a.S <= bh::MAXS; }
+// D = 32, S <= 256 and the tiled kernels' layout conditions (bwd_tiled_ok);
+// with stored probs also S % 4 == 0 and 16-byte aligned probs (phase 1 reads
+// them as 16-byte pieces).
+inline bool bh_ok(const BwdArgs& a) {
+    if (a.D != bh::D || a.S < 1 || a.S > bh::MAXS) return false;
+    return !a.probs || (a.S % 4 == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15u) == 0);
+}
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool PROBS>
 hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    auto kern = bh::bwd_bh_kernel<CAUSAL>;
+    auto kern = bh::bwd_bh_kernel<CAUSAL, PROBS>;
     // The dynamic-LDS limit is raised once per device (bit d of attr_set).
     static std::atomic<unsigned long long> attr_set{0};
     int dev = 0;
@@ -350,7 +466,8 @@ hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
 }
 
 inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
-    return a.causal ? launch_bh_mode<true>(a, s) : launch_bh_mode<false>(a, s);
+    if (a.probs) return a.causal ? launch_bh_mode<true, true>(a, s) : launch_bh_mode<false, true>(a, s);
+    return a.causal ? launch_bh_mode<true, false>(a, s) : launch_bh_mode<false, false>(a, s);
 }
 
 }  // namespace bwd

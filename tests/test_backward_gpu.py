@@ -40,11 +40,14 @@ def _inputs(B, S, E, H, causal=False, seed=0):
 
 
 # D = 32/64/128 MFMA kernels, padded D (7, 16, 48, 96), generic D (160, 256),
-# S below / across / not a multiple of the 32-row tile.
+# S below / across / not a multiple of the 32-row tile.  D = 32 with S % 4 == 0
+# and S <= 256 runs the one-workgroup-per-(b, h) kernel (S = 4, 32, 44, 100,
+# 256); other D = 32 shapes the query/key-stationary pair.
 SHAPES = [
     (1, 1, 32, 1), (2, 7, 64, 2), (1, 33, 128, 2), (2, 64, 256, 2), (1, 100, 96, 2),
     (1, 45, 32, 2), (1, 70, 192, 2), (1, 40, 512, 2), (1, 9, 14, 2), (2, 300, 256, 4),
     (1, 129, 128, 1), (1, 20, 320, 2),
+    (2, 4, 64, 2), (1, 32, 64, 2), (3, 44, 128, 4), (2, 100, 128, 4), (1, 256, 256, 8), (1, 260, 64, 2),
 ]
 
 
@@ -76,7 +79,7 @@ def test_drop_in_backward_matches_reference_kernel(dev, B, S, E, H):
 
 
 @pytest.mark.parametrize("B,S,E,H", [(2, 37, 64, 2), (1, 160, 128, 2), (2, 96, 256, 2), (1, 75, 96, 1),
-                                     (1, 50, 512, 2)])
+                                     (1, 50, 512, 2), (2, 96, 64, 2), (1, 228, 256, 8), (1, 36, 32, 1)])
 def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     """Causal probs: the extended entry point with causal=1 skips tiles above
     the diagonal; the skipped terms are exact zeros, so the result equals the
