@@ -32,10 +32,12 @@
 // PROBS (the stored [S][S] probs instead of O and lse): P is read from
 // memory instead of rebuilt, and Dq = sum_j P_ij dP_ij = dO_i . (P V)_i needs
 // O = P V first.  Phase 1 forms it along the same chain (each key tile adds
-// its P V term, 16 MFMAs per job, the finished rows staying in LDS); after a
-// workgroup barrier every thread forms Dq for its rows, and after a second
-// barrier phase 2 runs the jobs above with the loaded P.  80 MFMAs per job as
-// in the probs-free mode; P is read twice (once per phase).
+// its P V term, 16 MFMAs per job); the last contributor of a query tile forms
+// its rows' Dq and flags them, and phase 2 (the jobs above, with the loaded
+// P) waits per tile for that flag.  Causally the light wave of each SIMD
+// pair also runs its heavy partner's phase-1 jobs, so the wave with the most
+// phase-2 jobs starts them at once.  80 MFMAs per job as in the probs-free
+// mode; P is read twice (once per phase).
 //
 // One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
@@ -109,6 +111,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     __shared__ int staged[NW];  // query tile t's rows are in LDS
     __shared__ int chain[NW];   // contributions summed into query tile t's dQ partial
     __shared__ int ochain[NW];  // stored probs: contributions summed into query tile t's O partial
+    __shared__ int dqready[NW]; // stored probs: Dq of query tile t is in LDS
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, hf = lane >> 5;
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     float* const X = lds + L.x + wave * BK * XP;
     const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
 
-    if (tid < NW) staged[tid] = chain[tid] = ochain[tid] = 0;
+    if (tid < NW) staged[tid] = chain[tid] = ochain[tid] = dqready[tid] = 0;
     // Key tile of this wave: SIMD s (ranks 2s, 2s+1) takes tiles s and
     // nt-1-s, so causal work pairs up to nt + 1 tiles per SIMD.  The rank's
     // barrier also publishes the cleared flags.
@@ -132,9 +135,13 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const int s2 = sr >> 1;
     int kt = -1;
     if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
-    // (stored probs: idle waves stay for the workgroup barriers below)
-    if (!PROBS && kt < 0) return;
-    const bool active = kt >= 0;
+    if (kt < 0) return;
+    // Stored probs, causal: the SIMD's light wave (key tile nt-1-s2, s2 + 1
+    // jobs) also runs the phase-1 jobs of the heavy one (key tile s2), which
+    // goes straight to phase 2.
+    const bool light = PROBS && CAUSAL && (sr & 1);
+    const bool p1_off = PROBS && CAUSAL && !(sr & 1) && nt - 1 - s2 > s2;
+    const int kp = s2;  // a light wave's partner
 
     // Causal: key tile kt first needs query tile kt + t at its step t, and the
     // wave of key tile 0 has the most steps.  Starting wave kt's loads kt
@@ -158,9 +165,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // back through the scratch.  Every global load is issued before the
     // first use (one round trip); rows past S load as zero.
     const int kj = kt * BK + c;
-    const bool kval = active && kj < S;
-    float kr2[D / 2], vr[D / 2], kq[16], vq[PROBS ? 16 : 1];
-    if (active) {
+    const bool kval = kj < S;
+    float kr2[D / 2], vr[D / 2], kq[16], vq[PROBS ? 16 : 1], vq2[PROBS ? 16 : 1];
+    {
         RowLoader ql, gl, ol, kl, vl;
         ql.init(a.q + base, a.ts, S, D);
         gl.init(a.go + base, a.ts, S, D);
@@ -218,9 +225,18 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = vv[s];
 #pragma unroll
             for (int s = 0; s < 16; ++s) vq[s] = X[dq_key(s, hf) * XP + c];
+            if (light) {  // and the partner's V
+                floatx4 v2[D / 8];
+#pragma unroll
+                for (int s = 0; s < D / 8; ++s) v2[s] = vl.load(kp * BK + c, hf * (D / 8) + s);
+#pragma unroll
+                for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = v2[s];
+#pragma unroll
+                for (int s = 0; s < 16; ++s) vq2[s] = X[dq_key(s, hf) * XP + c];
+            }
         }
     }
-    if (!PROBS) set_flag(&staged[kt], 1);
+    set_flag(&staged[kt], 1);
 
     const bool kedge = kt * BK + BK > S;  // keys past S in this tile
     const int nsteps = CAUSAL ? nt - kt : nt;
@@ -232,63 +248,80 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 
     if constexpr (PROBS) {
         // Phase 1: O = P V summed over key tiles along the same chain as dQ
-        // (step t: query tile kt + t), the last contributor leaving the
-        // finished rows in the partial buffer; then Dq = dO . O per row.
-        if (active) {
-            // P[query i*32 + c][key kt*32 + dq_key(s, h)] for s = 8u + 4w + j;
+        // (step t of key tile k: query tile k + t).  The last contributor of
+        // tile i forms Dq = dO . O for its rows and flags them; phase 2's jobs
+        // on tile i wait for that flag.
+        // P[query i*32 + c][key k*32 + dq_key(s, h)] for s = 8u + 4w + j
+        auto load_pa = [&](floatx4 (&pa)[4], int k, int i) {
+            const int vo = (i * BK + c) * S4 + (k * BK + 8 * hf) * 4;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    const floatx4 v = __builtin_bit_cast(
+                        floatx4, __builtin_amdgcn_raw_buffer_load_b128(pr, vo + (16 * u + 4 * w) * 4, 0, 0));
+                    pa[2 * u + w] = (k * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+        };
+        auto p1_job = [&](const floatx4 (&pa)[4], const float (&vk)[16], int i, int t) {
+            floatx16 o;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[s >> 2][s & 3], vk[s], o, 0, 0, 0);
+            const int nc = CAUSAL ? i + 1 : nt;
+            float* const part = DQA + (i * BK + 4 * hf) * PP + c;
+            if (t > 0) {
+                wait_ge(&ochain[i], t);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[r] += part[(8 * (r >> 2) + (r & 3)) * PP];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = o[r];
+            if (t < nc - 1) {
+                set_flag(&ochain[i], t + 1);
+            } else {
+                // Dq of the tile's rows: lane pair (2r, 2r+1) takes row r's halves
+                wait_ge(&staged[i], 1);
+                const int row = i * BK + (lane >> 1), h16 = (lane & 1) * 16;
+                float d = 0.f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const floatx4 o4 = *reinterpret_cast<const floatx4*>(DQA + row * PP + h16 + 4 * k);
+                    const floatx4 g4 = *reinterpret_cast<const floatx4*>(Gr + row * RP + h16 + 4 * k);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) d = fmaf(g4[j], o4[j], d);
+                }
+                d += __shfl_xor(d, 1);
+                if (!(lane & 1)) DV[row] = d;
+                set_flag(&dqready[i], 1);
+            }
+        };
+        if (light) {
+            // own jobs (key kt, nt - kt of them) and the partner's (key kp < kt), by step
+            for (int t = 0; t < nt - kp; ++t) {
+                floatx4 pa[4];
+                if (t < nt - kt) {
+                    load_pa(pa, kt, kt + t);
+                    p1_job(pa, vq, kt + t, t);
+                }
+                load_pa(pa, kp, kp + t);
+                p1_job(pa, vq2, kp + t, t);
+            }
+        } else if (!p1_off) {
             // the next job's tile is requested before this one's products
-            auto load_pa = [&](floatx4 (&pa)[4], int i) {
-                const int vo = (i * BK + c) * S4 + (kt * BK + 8 * hf) * 4;
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-#pragma unroll
-                    for (int w = 0; w < 2; ++w) {
-                        const floatx4 v = __builtin_bit_cast(
-                            floatx4, __builtin_amdgcn_raw_buffer_load_b128(pr, vo + (16 * u + 4 * w) * 4, 0, 0));
-                        pa[2 * u + w] = (kt * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
-                    }
-            };
             floatx4 pn[4];
-            load_pa(pn, kt);
+            load_pa(pn, kt, kt);
             for (int t = 0; t < nsteps; ++t) {
                 int i = kt + t;
                 if (!CAUSAL && i >= nt) i -= nt;
                 floatx4 pa[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) pa[k] = pn[k];
-                if (t + 1 < nsteps) load_pa(pn, i + 1 < nt ? i + 1 : 0);
-                floatx16 o;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[r] = 0.f;
-#pragma unroll
-                for (int s = 0; s < 16; ++s) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[s >> 2][s & 3], vq[s], o, 0, 0, 0);
-                const int nc = CAUSAL ? i + 1 : nt;
-                float* const part = DQA + (i * BK + 4 * hf) * PP + c;
-                if (t > 0) {
-                    wait_ge(&ochain[i], t);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[r] += part[(8 * (r >> 2) + (r & 3)) * PP];
-                }
-#pragma unroll
-                for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = o[r];
-                if (t < nc - 1) set_flag(&ochain[i], t + 1);
+                if (t + 1 < nsteps) load_pa(pn, kt, i + 1 < nt ? i + 1 : 0);
+                p1_job(pa, vq, i, t);
             }
         }
-        __syncthreads();
-        // Sp * CPR is a multiple of 256: a wave's lanes are all in or all out
-        for (int f = tid; f < Sp * CPR; f += NW * 64) {
-            const int row = f / CPR, cc = f % CPR;
-            const floatx4 o4 = *reinterpret_cast<const floatx4*>(DQA + row * PP + 4 * cc);
-            const floatx4 g4 = *reinterpret_cast<const floatx4*>(Gr + row * RP + 4 * cc);
-            float d = g4[0] * o4[0];
-#pragma unroll
-            for (int j = 1; j < 4; ++j) d = fmaf(g4[j], o4[j], d);
-#pragma unroll
-            for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
-            if (cc == 0) DV[row] = d;
-        }
-        __syncthreads();
-        if (!active) return;
     }
 
     // Stored probs, phase 2: P of query tile i in the accumulator's order
@@ -352,7 +385,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         constexpr bool HP = decltype(has_prev)::value;
         int i = kt + t;
         if (!CAUSAL && i >= nt) i -= nt;
-        if (HP && !PROBS) wait_ge(&staged[i], 1);  // stored probs: staged before the barriers
+        if (PROBS)
+            wait_ge(&dqready[i], 1);  // implies tile i staged (its setter waited for that)
+        else if (HP)
+            wait_ge(&staged[i], 1);
         const float* qt = Qr + i * BK * RP;
         const float* gt = Gr + i * BK * RP;
         // The chains start from -lse' and -Dq, so they end at S' - lse' and
