@@ -48,6 +48,7 @@ SHAPES = [
     (1, 45, 32, 2), (1, 70, 192, 2), (1, 40, 512, 2), (1, 9, 14, 2), (2, 300, 256, 4),
     (1, 129, 128, 1), (1, 20, 320, 2),
     (2, 4, 64, 2), (1, 32, 64, 2), (3, 44, 128, 4), (2, 100, 128, 4), (1, 256, 256, 8), (1, 260, 64, 2),
+    (4, 64, 2560, 80),  # B*H = 320 workgroups: more than one per CU
 ]
 
 
