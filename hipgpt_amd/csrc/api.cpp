@@ -119,7 +119,8 @@ void launch_attention_weighted_sum(const float* softmax, const float* V, float* 
 // Attention backward (src/hip_kernels.cpp:1245-1272).  The planar buffers of
 // the forward; the B*H*S row-dot workspace comes from the caller or, for the
 // drop-in symbol (whose signature has no workspace), from a buffer cached per
-// device and grown on demand.
+// device and grown on demand -- only for shapes whose kernels use it (not
+// D = 32 with S <= 256, S % 4 == 0, which forms the row dots in LDS).
 namespace {
 
 hipgpt::BwdArgs planar_bwd_args(const float* go, const float* qkv, const float* probs, float* gqkv, int B, int S,
@@ -173,10 +174,12 @@ void launch_multihead_attention_backward(const float* d_grad_attn_output, const 
     }
     if (B <= 0 || S <= 0 || E <= 0) return;
     hipgpt::BwdArgs a = planar_bwd_args(d_grad_attn_output, d_qkv, d_softmax, d_grad_qkv, B, S, E, H, 0);
-    a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
-    if (!a.dvec) {
-        fprintf(stderr, "launch_multihead_attention_backward: workspace allocation failed\n");
-        return;
+    if (hipgpt::bwd_uses_workspace(a)) {  // HipGPT's default shape (D = 32, S <= 256) needs none
+        a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
+        if (!a.dvec) {
+            fprintf(stderr, "launch_multihead_attention_backward: workspace allocation failed\n");
+            return;
+        }
     }
     report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
 }

@@ -328,6 +328,8 @@ bool bwd_tiled_ok(const BwdArgs& a) {
            ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
 }
 
+bool bwd_uses_workspace(const BwdArgs& a) { return a.probs && !(bwd_tiled_ok(a) && bwd::bh_ok(a)); }
+
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     // recompute mode (no probs): tiled kernels only
     if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;

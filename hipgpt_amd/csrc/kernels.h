@@ -62,6 +62,9 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s);
 // The LDS-tiled MFMA kernels apply (D = 32 or 64, 16-byte aligned rows); the
 // only backward path for recompute mode.
 bool bwd_tiled_ok(const BwdArgs& a);
+// False when launch_attn_bwd takes a path that needs no dvec workspace (the
+// one-workgroup-per-(b, h) kernel, or recompute mode).
+bool bwd_uses_workspace(const BwdArgs& a);
 
 // Unfused single-head helpers (HipGPT src/hip_kernels.cpp:454-532).
 hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int S, int D, hipStream_t s);
