@@ -123,6 +123,14 @@ __device__ __forceinline__ void store_probs_tile(float* prow, const floatx16& p,
     }
 }
 
+// Causal probs, streaming kernel: the zeros above the diagonal are stored
+// before the sweeps (1; c1 with probs 26.5 -> 25.2 us) or after them (0).  The
+// resident kernel stores them last: its start is already HBM-bound, and
+// storing them first measured slower there (c2 with probs 46.7 -> 48.3 us).
+#ifndef HIPGPT_ZERO_FIRST
+#define HIPGPT_ZERO_FIRST 1
+#endif
+
 // Causal: zero the probs of this wave's queries for keys >= z0.
 __device__ __forceinline__ void zero_probs_tail(float* probs_bh, int qw0, int Sq, int Sk, int z0, int lane, bool pvec) {
     for (int r = 0; r < QW; ++r) {

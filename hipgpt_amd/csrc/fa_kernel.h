@@ -389,6 +389,14 @@ struct FaKernel {
                 }
             }
         } else {
+#if HIPGPT_ZERO_FIRST
+            // Causal: the zeros above the diagonal need no data, so they are
+            // stored before the sweeps, while the first stage's loads are in flight.
+            if (CAUSAL && qw0 < Sq && ks == 0) {
+                const bool pv0 = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
+                zero_probs_tail(a.probs + (int64_t)bh * Sq * Sk, qw0, Sq, Sk, tr.wtiles * BK, lane, pv0);
+            }
+#endif
             if constexpr (SRT > 0)
                 sweep_res(std::false_type{}, 0.f, nullptr, false);
             else
@@ -415,7 +423,7 @@ struct FaKernel {
                 sweep_res(std::true_type{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
             else
                 sweep(std::integral_constant<int, 2>{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
-            if (CAUSAL && qw0 < Sq && ks == 0) {
+            if (!HIPGPT_ZERO_FIRST && CAUSAL && qw0 < Sq && ks == 0) {
                 const int ztile = tr.wtiles;  // tiles [0, wtiles) were written by the NKS waves
                 zero_probs_tail(probs_bh, qw0, Sq, Sk, ztile * BK, lane, pvec);
             }
