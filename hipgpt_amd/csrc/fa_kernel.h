@@ -230,7 +230,7 @@ struct FaKernel {
         // One stage of compute on LDS buffer (i & 1).  MODE 0: online softmax
         // + PV.  MODE 1: max/sum only.  MODE 2: probs store + PV with the
         // final (m, l).
-        auto compute = [&](auto mode_tag, int i, float linv, float* prow, bool pvec) {
+        auto compute = [&](auto mode_tag, int i, float mlog, float* prow, bool pvec) {
             constexpr int MODE = decltype(mode_tag)::value;
             const E* cur = lds + (i & 1) * STAGE_ELEMS;
             const int t = i * NKS + ks;
@@ -269,7 +269,7 @@ struct FaKernel {
                 m_run = m_new;
             } else {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -m_run)) * linv;
+                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -mlog));
                 if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 TR::pv(vreg, s, o, c, hf);
             }
@@ -280,7 +280,7 @@ struct FaKernel {
         // requested while stage i is computed and stage i+1 (requested one
         // stage earlier) is written to LDS afterwards, so every global load
         // has two stages of compute to land.
-        auto sweep = [&](auto mode_tag, float linv, float* prow, bool pvec) {
+        auto sweep = [&](auto mode_tag, float mlog, float* prow, bool pvec) {
             constexpr bool WV = decltype(mode_tag)::value != 1;  // the max/sum sweep stages no V
             if (nstages > 0) {
                 st.template load<0, WV>(0, tid);
@@ -292,7 +292,7 @@ struct FaKernel {
                 constexpr int SL = decltype(slot_tag)::value;  // slot free for new loads
                 constexpr int NX = PF == 2 ? 1 - SL : 0;      // slot holding stage i+1
                 if (i + PF < nstages) st.template load<SL, WV>(i + PF, tid);
-                compute(mode_tag, i, linv, prow, pvec);
+                compute(mode_tag, i, mlog, prow, pvec);
                 if (i + 1 < nstages) st.template store<NX, WV>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
                 __syncthreads();
             };
@@ -305,7 +305,7 @@ struct FaKernel {
         // Score-resident probs sweeps (SRT > 0).  Stage I holds tile I*NKS + ks
         // of this wave; sres[I] keeps its masked scores between the sweeps.
         floatx16 sres[SRT > 0 ? SRT : 1];
-        auto sweep_res = [&](auto second_tag, float linv, float* prow, bool pvec) {
+        auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
             if (nstages > 0) {
                 st.template load<0, SECOND, !SECOND>(0, tid);
@@ -334,7 +334,7 @@ struct FaKernel {
                                 TR::load_v(vreg, vt_of(cur, t), c, hf);
                                 floatx16 p = sres[I];
 #pragma unroll
-                                for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -m_run)) * linv;
+                                for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -mlog));
                                 if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
                                 TR::pv(vreg, p, o, c, hf);
                             }
@@ -416,13 +416,15 @@ struct FaKernel {
                 l_run = L;
                 __syncthreads();  // the stage buffers overwrite the slots next
             }
-            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            // P = exp2(s' - m) / l = exp2(s' - (m + log2 l)): the normalisation
+            // rides in the exponent (no multiply per score)
+            const float mlog = m_run + __builtin_amdgcn_logf(fmaxf(l_run, 1e-20f));
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
             const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
             if constexpr (SRT > 0)
-                sweep_res(std::true_type{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
+                sweep_res(std::true_type{}, mlog, probs_bh + (int64_t)qi * Sk, pvec);
             else
-                sweep(std::integral_constant<int, 2>{}, linv, probs_bh + (int64_t)qi * Sk, pvec);
+                sweep(std::integral_constant<int, 2>{}, mlog, probs_bh + (int64_t)qi * Sk, pvec);
             if (!HIPGPT_ZERO_FIRST && CAUSAL && qw0 < Sq && ks == 0) {
                 const int ztile = tr.wtiles;  // tiles [0, wtiles) were written by the NKS waves
                 zero_probs_tail(probs_bh, qw0, Sq, Sk, ztile * BK, lane, pvec);

@@ -272,7 +272,8 @@ struct FaResident {
                 l_run = L2;
             }
             // sweep 2 from the resident tiles: P = exp(s - m) / l stored once, P V
-            const float linv = 1.0f / fmaxf(l_run, 1e-20f);
+            // P = exp2(s' - (m + log2 l)): the normalisation rides in the exponent
+            const float mlog = m_run + __builtin_amdgcn_logf(fmaxf(l_run, 1e-20f));
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
             float* prow = probs_bh + (int64_t)qi * Sk;
             const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
@@ -281,7 +282,7 @@ struct FaResident {
                 typename TR::VReg vreg;
                 TR::load_v(vreg, tiles + t * TILE_ELEMS + TR::KTILE, c, hf);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -m_run)) * linv;
+                for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -mlog));
                 if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 TR::pv(vreg, s, o, c, hf);
             }
