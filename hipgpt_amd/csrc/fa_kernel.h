@@ -258,7 +258,7 @@ struct FaKernel {
                     s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
                     ls += s[r];
                 }
-                l_run += halves_sum(ls);
+                l_run += ls;  // this lane half's partial; the halves are summed after the sweep
                 TR::pv(vreg, s, o, c, hf);
             } else if (MODE == 1) {
                 const float m_new = vmax(m_run, tile_max(s) * sc);
@@ -354,6 +354,7 @@ struct FaKernel {
 
         if (!PROBS) {
             sweep(std::integral_constant<int, 0>{}, 0.f, nullptr, false);
+            l_run = halves_sum(l_run);
             if (NKS > 1) {
                 // wave ks > 0 publishes (m, l, O); wave ks == 0 merges
                 if (ks != 0) {

@@ -192,7 +192,7 @@ struct FaResident {
                 s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
                 ls += s[r];
             }
-            l_run += halves_sum(ls);
+            l_run += ls;  // this lane half's partial; the halves are summed after the loop
             TR::pv(vreg, s, o, c, hf);
         };
         auto stats = [&](int t) {
@@ -256,6 +256,7 @@ struct FaResident {
             }
         }
 
+        if (!PROBS) l_run = halves_sum(l_run);
         float* const ml = reinterpret_cast<float*>(lds_raw + 256);  // [NW][2][64]
         if (PROBS) {
             if (NKS > 1) {  // combine the splits' (m, l): every split needs the row's final values
