@@ -31,13 +31,13 @@
 //
 // PROBS (the stored [S][S] probs instead of O and lse): P is read from
 // memory instead of rebuilt, and Dq = sum_j P_ij dP_ij = dO_i . (P V)_i needs
-// O = P V first.  Phase 1 forms it along the same chain (each key tile adds
-// its P V term, 16 MFMAs per job); the last contributor of a query tile forms
-// its rows' Dq and flags them, and phase 2 (the jobs above, with the loaded
-// P) waits per tile for that flag.  Causally the light wave of each SIMD
-// pair also runs its heavy partner's phase-1 jobs, so the wave with the most
-// phase-2 jobs starts them at once.  80 MFMAs per job as in the probs-free
-// mode; P is read twice (once per phase).
+// O = P V first.  Phase 1 gives each query tile's O to one wave, which sums
+// the key tiles' P V terms in registers (16 MFMAs per key tile, V rows read
+// as it goes), forms the tile's Dq and flags it; phase 2 (the jobs above,
+// with the loaded P) waits per tile for that flag.  Causally the light wave
+// of each SIMD pair owns both of the pair's query tiles, the heavy partner's
+// first, so the wave with the most phase-2 jobs starts them at once.  P is
+// read twice (once per phase).
 //
 // One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
@@ -110,7 +110,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     __shared__ int simd_slots[NW];
     __shared__ int staged[NW];  // query tile t's rows are in LDS
     __shared__ int chain[NW];   // contributions summed into query tile t's dQ partial
-    __shared__ int ochain[NW];  // stored probs: contributions summed into query tile t's O partial
     __shared__ int dqready[NW]; // stored probs: Dq of query tile t is in LDS
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -127,7 +126,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     float* const X = lds + L.x + wave * BK * XP;
     const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
 
-    if (tid < NW) staged[tid] = chain[tid] = ochain[tid] = dqready[tid] = 0;
+    if (tid < NW) staged[tid] = chain[tid] = dqready[tid] = 0;
     // Key tile of this wave: SIMD s (ranks 2s, 2s+1) takes tiles s and
     // nt-1-s, so causal work pairs up to nt + 1 tiles per SIMD.  The rank's
     // barrier also publishes the cleared flags.
@@ -137,7 +136,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
     if (kt < 0) return;
     // Stored probs, causal: the SIMD's light wave (key tile nt-1-s2, s2 + 1
-    // jobs) also runs the phase-1 jobs of the heavy one (key tile s2), which
+    // jobs) runs the phase-1 work of both tiles; the heavy one (key tile s2)
     // goes straight to phase 2.
     const bool light = PROBS && CAUSAL && (sr & 1);
     const bool p1_off = PROBS && CAUSAL && !(sr & 1) && nt - 1 - s2 > s2;
@@ -160,13 +159,13 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // Stage query tile kt: Q and dO rows, and (recompute) Dq = dO . O and
     // lse' = lse log2 e (+inf past S: P = 0 there); and the wave's keys: K
     // pre-scaled to log2 units and V (B operands of S' and dP, lane (c, h)
-    // holds dims 16h .. 16h+15 of key kj), K (and, stored probs, V) as the B
-    // operand of a product over keys (step s: key dq_key(s, h), dim c), read
-    // back through the scratch.  Every global load is issued before the
+    // holds dims 16h .. 16h+15 of key kj), K as the B operand of a product
+    // over keys (step s: key dq_key(s, h), dim c), read back through the
+    // scratch.  Every global load is issued before the
     // first use (one round trip); rows past S load as zero.
     const int kj = kt * BK + c;
     const bool kval = kj < S;
-    float kr2[D / 2], vr[D / 2], kq[16], vq[PROBS ? 16 : 1], vq2[PROBS ? 16 : 1];
+    float kr2[D / 2], vr[D / 2], kq[16];
     {
         RowLoader ql, gl, ol, kl, vl;
         ql.init(a.q + base, a.ts, S, D);
@@ -219,22 +218,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s) kq[s] = X[dq_key(s, hf) * XP + c];
-        if constexpr (PROBS) {
-            // V the same way, after the K reads (a wave's LDS accesses run in order)
-#pragma unroll
-            for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = vv[s];
-#pragma unroll
-            for (int s = 0; s < 16; ++s) vq[s] = X[dq_key(s, hf) * XP + c];
-            if (light) {  // and the partner's V
-                floatx4 v2[D / 8];
-#pragma unroll
-                for (int s = 0; s < D / 8; ++s) v2[s] = vl.load(kp * BK + c, hf * (D / 8) + s);
-#pragma unroll
-                for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = v2[s];
-#pragma unroll
-                for (int s = 0; s < 16; ++s) vq2[s] = X[dq_key(s, hf) * XP + c];
-            }
-        }
     }
     set_flag(&staged[kt], 1);
 
@@ -247,79 +230,103 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const int S4 = S * 4;
 
     if constexpr (PROBS) {
-        // Phase 1: O = P V summed over key tiles along the same chain as dQ
-        // (step t of key tile k: query tile k + t).  The last contributor of
-        // tile i forms Dq = dO . O for its rows and flags them; phase 2's jobs
-        // on tile i wait for that flag.
-        // P[query i*32 + c][key k*32 + dq_key(s, h)] for s = 8u + 4w + j
-        auto load_pa = [&](floatx4 (&pa)[4], int k, int i) {
-            const int vo = (i * BK + c) * S4 + (k * BK + 8 * hf) * 4;
+        // Phase 1: O = P V of whole query tiles, each owned by one wave that
+        // sums its key tiles in ascending order (causally the keys past the
+        // diagonal add exact zeros last, so causal and non-causal agree bit for
+        // bit), then forms the tile's Dq = dO . O and flags it; phase 2's jobs
+        // on a tile wait for that flag.  The product is formed transposed, so V
+        // rows load straight into the A operand and each lane ends with its
+        // query's O for the Dq sum (no LDS round trip).  Causally the light wave of SIMD s
+        // (key tile nt-1-s) owns query tiles s and nt-1-s (s+1 and nt-s
+        // jobs: nt+1 per SIMD), tile s first, the one its heavy partner
+        // starts on; the heavy wave owns none.  Otherwise a wave owns its
+        // key tile's index.
+        // P[query i*32 + c][key j*32 + dq_key(s, h)] for s = 8u + 4w + e
+        auto load_pa = [&](floatx4 (&pa)[4], int j, int i) {
+            const int vo = (i * BK + c) * S4 + (j * BK + 8 * hf) * 4;
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int w = 0; w < 2; ++w) {
                     const floatx4 v = __builtin_bit_cast(
                         floatx4, __builtin_amdgcn_raw_buffer_load_b128(pr, vo + (16 * u + 4 * w) * 4, 0, 0));
-                    pa[2 * u + w] = (k * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                    pa[2 * u + w] = (j * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
                 }
         };
-        auto p1_job = [&](const floatx4 (&pa)[4], const float (&vk)[16], int i, int t) {
-            floatx16 o;
+        // O^T = V^T P^T: the A operand at step s is V[key j*32 + dq_key(s, h)][dim c],
+        // one coalesced dword per lane (rows past S read as zero)
+        RowLoader vl1;
+        vl1.init(a.v + base, a.ts, S, D);
+        auto load_v = [&](float (&vv)[16], int j) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[r] = 0.f;
+            for (int e = 0; e < 16; ++e)
+                vv[e] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(vl1.rs, (j * BK + dq_key(e, hf)) * vl1.row_bytes + c * 4, 0, 0));
+        };
+        int tiles[2], ntl = 0;
+        if (light) {
+            tiles[0] = kp;
+            tiles[1] = kt;
+            ntl = 2;
+        } else if (!p1_off) {
+            tiles[0] = kt;
+            ntl = 1;
+        }
+        auto tile_of = [&](int n, int& jn) {  // job n -> (tile, key tile jn)
+            const int len0 = CAUSAL ? tiles[0] + 1 : nt;
+            if (n < len0) {
+                jn = n;
+                return tiles[0];
+            }
+            jn = n - len0;
+            return tiles[1];
+        };
+        const int njobs = ntl == 0 ? 0 : (CAUSAL ? tiles[0] + 1 : nt) + (ntl == 2 ? (CAUSAL ? tiles[1] + 1 : nt) : 0);
+        floatx4 pn[4];
+        float vn[16];
+        if (njobs > 0) {
+            int j0;
+            const int i0 = tile_of(0, j0);
+            load_pa(pn, j0, i0);
+            load_v(vn, j0);
+        }
+        floatx16 o;  // register r <-> dim acc_key(r, h), lane <-> query i*32 + c
 #pragma unroll
-            for (int s = 0; s < 16; ++s) o = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[s >> 2][s & 3], vk[s], o, 0, 0, 0);
-            const int nc = CAUSAL ? i + 1 : nt;
-            float* const part = DQA + (i * BK + 4 * hf) * PP + c;
-            if (t > 0) {
-                wait_ge(&ochain[i], t);
+        for (int r = 0; r < 16; ++r) o[r] = 0.f;
+        for (int n = 0; n < njobs; ++n) {
+            int jn;
+            const int i = tile_of(n, jn);
+            floatx4 pa[4];
+            float vv[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o[r] += part[(8 * (r >> 2) + (r & 3)) * PP];
+            for (int u = 0; u < 4; ++u) pa[u] = pn[u];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) vv[e] = vn[e];
+            if (n + 1 < njobs) {  // the next job's tiles are requested before this one's products
+                int j1;
+                const int i1 = tile_of(n + 1, j1);
+                load_pa(pn, j1, i1);
+                load_v(vn, j1);
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = o[r];
-            if (t < nc - 1) {
-                set_flag(&ochain[i], t + 1);
-            } else {
-                // Dq of the tile's rows: lane pair (2r, 2r+1) takes row r's halves
+            for (int e = 0; e < 16; ++e) o = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[e], pa[e >> 2][e & 3], o, 0, 0, 0);
+            int jl;
+            if (n + 1 == njobs || tile_of(n + 1, jl) != i) {
+                // tile i complete: Dq of query i*32 + c over this half's 16 dims, then the halves summed
                 wait_ge(&staged[i], 1);
-                const int row = i * BK + (lane >> 1), h16 = (lane & 1) * 16;
+                const float* const g = Gr + (i * BK + c) * RP + 4 * hf;
                 float d = 0.f;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const floatx4 o4 = *reinterpret_cast<const floatx4*>(DQA + row * PP + h16 + 4 * k);
-                    const floatx4 g4 = *reinterpret_cast<const floatx4*>(Gr + row * RP + h16 + 4 * k);
+                    const floatx4 g4 = *reinterpret_cast<const floatx4*>(g + 8 * k);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) d = fmaf(g4[j], o4[j], d);
+                    for (int e = 0; e < 4; ++e) d = fmaf(g4[e], o[4 * k + e], d);
                 }
-                d += __shfl_xor(d, 1);
-                if (!(lane & 1)) DV[row] = d;
+                d += __shfl_xor(d, 32);
+                if (!hf) DV[i * BK + c] = d;
                 set_flag(&dqready[i], 1);
-            }
-        };
-        if (light) {
-            // own jobs (key kt, nt - kt of them) and the partner's (key kp < kt), by step
-            for (int t = 0; t < nt - kp; ++t) {
-                floatx4 pa[4];
-                if (t < nt - kt) {
-                    load_pa(pa, kt, kt + t);
-                    p1_job(pa, vq, kt + t, t);
-                }
-                load_pa(pa, kp, kp + t);
-                p1_job(pa, vq2, kp + t, t);
-            }
-        } else if (!p1_off) {
-            // the next job's tile is requested before this one's products
-            floatx4 pn[4];
-            load_pa(pn, kt, kt);
-            for (int t = 0; t < nsteps; ++t) {
-                int i = kt + t;
-                if (!CAUSAL && i >= nt) i -= nt;
-                floatx4 pa[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) pa[k] = pn[k];
-                if (t + 1 < nsteps) load_pa(pn, kt, i + 1 < nt ? i + 1 : 0);
-                p1_job(pa, vq, i, t);
+                for (int r = 0; r < 16; ++r) o[r] = 0.f;
             }
         }
     }

@@ -3,8 +3,8 @@ backward (hipgpt_amd/csrc/bwd_bh.h).
 
 The kernel's waves wait on LDS flags instead of workgroup barriers: a tile's
 "staged" flag, the dQ chain counter of a query tile (contributions in
-descending key-tile order), and with stored probs the O chain counter and the
-per-tile "Dq ready" flag.  Every wait is bounded on the device, but a schedule
+descending key-tile order), and with stored probs the per-tile "Dq ready"
+flag.  Every wait is bounded on the device, but a schedule
 that could block would silently produce wrong gradients, so this test restates
 each wave's sequence of waits and sets (the same key-tile assignment, job
 order and flags as the kernel) and runs them under an event scheduler that
@@ -16,9 +16,10 @@ a wave blocked with nothing else runnable.
 Restated from: key-tile assignment (sr -> kt, SIMD pairs s / nt-1-s), the
 staging flags, job(): step t handles query tile kt + t (mod nt if not
 causal), chain_add(): waits chain[i] >= t and sets t + 1 unless last; PROBS:
-light waves run the partner's phase-1 jobs by step, p1_job() waits
-ochain[i] >= t, the last contributor waits staged[i] and sets dqready[i];
-phase-2 jobs wait dqready[i].
+phase 1 gives query tile i's O to one wave (causally the light wave of the
+SIMD pair owns the partner's tile, then its own; the heavy wave none; else a
+wave owns its key tile's index), which waits staged[i] once the tile's O is
+summed and sets dqready[i]; phase-2 jobs wait dqready[i].
 """
 import random
 
@@ -45,26 +46,11 @@ def wave_programs(nt, causal, probs):
             i = k + t
             return i - nt if (not causal and i >= nt) else i
 
-        def p1_job(k, t):
-            i = tile(k, t)
-            nc = i + 1 if causal else nt
-            if t > 0:
-                ops.append(("wait", "ochain", i, t))
-            if t < nc - 1:
-                ops.append(("set", "ochain", i, t + 1))
-            else:
+        if probs:  # phase 1: no waits until a tile's O is summed in registers
+            owned = [kp, kt] if light else ([] if p1_off else [kt])
+            for i in owned:
                 ops.append(("wait", "staged", i, 1))
                 ops.append(("set", "dqready", i, 1))
-
-        if probs:
-            if light:
-                for t in range(nt - kp):
-                    if t < nt - kt:
-                        p1_job(kt, t)
-                    p1_job(kp, t)
-            elif not p1_off:
-                for t in range(nsteps):
-                    p1_job(kt, t)
         # phase 2 (or the only phase): job t, its dQ term added one job later
         prev = None
         for t in range(nsteps):
@@ -125,6 +111,9 @@ def run(waves, nt, rng=None):
 def test_every_wait_ends(nt, causal, probs):
     waves = wave_programs(nt, causal, probs)
     assert sorted(kt for kt, _ in waves) == list(range(nt))  # each key tile owned once
+    if probs:  # each query tile's Dq formed once
+        sets = [i for _, ops in waves for kind, flag, i, _ in ops if kind == "set" and flag == "dqready"]
+        assert sorted(sets) == list(range(nt))
     for rng in [None] + [random.Random(seed) for seed in range(20)]:
         blocked, done = run(waves, nt, rng)
         assert not blocked, f"waves of key tiles {blocked} never finish"
