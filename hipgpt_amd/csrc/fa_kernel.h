@@ -34,6 +34,11 @@ namespace fa {
 // 100 MHz s_memrealtime counter = 200 ns per launch rank, for grids of at
 // most 4 query blocks per (batch, head).
 constexpr unsigned long long kStaggerTicks = 20;
+// The same for grids that write probs: 1 us per rank without a causal mask
+// (c1 drop-in 31.3 -> 29.9 us), 700 ns with one (c1 with probs 25.0 ->
+// 24.7 us); measured over 0.4 .. 1.6 us per rank.
+constexpr unsigned long long kStaggerTicksProbs = 100;
+constexpr unsigned long long kStaggerTicksProbsCausal = 70;
 constexpr int kStaggerMaxBlocks = 4;
 
 // Compile-time loop over I = 0 .. N-1 (each body sees I as a constant).
@@ -194,8 +199,12 @@ struct FaKernel {
         // when that burst has drained.  Launch rank r waits r * 200 ns first,
         // so the longest query blocks (rank 0) get their operands earliest
         // and compute while the shorter ones load (c1: 16.4 -> 15.9 us).
-        if (CAUSAL && a.n_qblk <= kStaggerMaxBlocks && rank > 0) {
-            const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)rank * kStaggerTicks;
+        // Writing probs, the ranks are spread further apart, so one rank's
+        // probs stores (the second sweep, HBM-bound) overlap the next rank's
+        // score sweep (MFMA-bound) instead of every workgroup storing at once.
+        if ((CAUSAL || PROBS) && a.n_qblk <= kStaggerMaxBlocks && rank > 0) {
+            const unsigned long long ticks = PROBS ? (CAUSAL ? kStaggerTicksProbsCausal : kStaggerTicksProbs) : kStaggerTicks;
+            const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)rank * ticks;
             for (int i = 0; i < 1024 && __builtin_amdgcn_s_memrealtime() < t_end; ++i) __builtin_amdgcn_s_sleep(2);
         }
         const TileRange tr = tile_range<CAUSAL>(q0, qw0, NQS * QW, Sq, Sk, off);
