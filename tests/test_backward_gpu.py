@@ -80,11 +80,14 @@ def test_drop_in_backward_matches_reference_kernel(dev, B, S, E, H):
 
 
 @pytest.mark.parametrize("B,S,E,H", [(2, 37, 64, 2), (1, 160, 128, 2), (2, 96, 256, 2), (1, 75, 96, 1),
-                                     (1, 50, 512, 2), (2, 96, 64, 2), (1, 228, 256, 8), (1, 36, 32, 1)])
+                                     (1, 50, 512, 2), (2, 96, 64, 2), (1, 228, 256, 8), (1, 36, 32, 1),
+                                     (2, 24, 32, 1), (1, 140, 64, 2), (1, 200, 128, 4)])
 def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     """Causal probs: the extended entry point with causal=1 skips tiles above
     the diagonal; the skipped terms are exact zeros, so the result equals the
-    unmasked drop-in bit for bit, and both match the oracle."""
+    unmasked drop-in bit for bit, and both match the oracle.  The D = 32 cases
+    with S % 4 == 0 run the one-workgroup-per-(b, h) kernel at 1, 2, 3, 5, 7
+    and 8 key tiles (odd counts leave a middle tile without a SIMD partner)."""
     qkv, go, probs = _inputs(B, S, E, H, causal=True, seed=3)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
