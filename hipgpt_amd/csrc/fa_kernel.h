@@ -30,10 +30,11 @@
 namespace hipgpt {
 namespace fa {
 
-// Start stagger of short causal grids (see FaKernel::run): 20 ticks of the
-// 100 MHz s_memrealtime counter = 200 ns per launch rank, for grids of at
-// most 4 query blocks per (batch, head).
-constexpr unsigned long long kStaggerTicks = 20;
+// Start stagger of short causal grids (see FaKernel::run): 35 ticks of the
+// 100 MHz s_memrealtime counter = 350 ns per launch rank, for grids of at
+// most 4 query blocks per (batch, head) (c1: 16.1 -> 15.8 us against 200 ns;
+// measured over 100 .. 800 ns per rank).
+constexpr unsigned long long kStaggerTicks = 35;
 // The same for grids that write probs: 1 us per rank without a causal mask
 // (c1 drop-in 31.3 -> 29.9 us), 700 ns with one (c1 with probs 25.0 ->
 // 24.7 us); measured over 0.4 .. 1.6 us per rank.
@@ -196,7 +197,7 @@ struct FaKernel {
         // Short causal problems (a few query blocks per (batch, head), the
         // whole grid resident at once) start with every workgroup loading its
         // first stage at the same moment, and the first tile computes only
-        // when that burst has drained.  Launch rank r waits r * 200 ns first,
+        // when that burst has drained.  Launch rank r waits r * 350 ns first,
         // so the longest query blocks (rank 0) get their operands earliest
         // and compute while the shorter ones load (c1: 16.4 -> 15.9 us).
         // Writing probs, the ranks are spread further apart, so one rank's
