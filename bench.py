@@ -4,15 +4,32 @@
 Headline (BASELINE.json metric): causal attention forward TFLOP/s and the
 fraction of the fp32 MFMA roofline at B32 H8 S256 D32 (config c1), inputs
 resident in HBM.  One step = one attention forward over the whole batch.
-The other BASELINE configs are timed the same way and reported under
-"configs"; the oracle's scalar restatement is timed on the host cores as
-"cpu_baseline".
+The other BASELINE configs, the drop-in contract (non-causal + probs, the
+call HipGPT makes) at every config, and the neighbouring kernels are timed
+the same way and reported under "configs"; the oracle's scalar restatement is
+timed on the host cores as "cpu_baseline" for c1..c5.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Timing protocol, per config:
+  * Input and output buffers are allocated in R independent sets, R chosen so
+    the sets together hold at least 1 GiB; timed calls rotate over the sets,
+    so a set is evicted from the 256 MB Infinity Cache (and every L2) before
+    it is used again and each call reads its operands from HBM.  This is
+    "us_per_call", the figure every rate and roofline fraction is computed
+    from.  "us_per_call_hot" repeats the calls on one set (operands can stay
+    in the Infinity Cache between calls).
+  * Both are means over exactly --steps back-to-back calls between two HIP
+    events on the launch stream, after >= 0.2 s of untimed calls (the GPU
+    needs ~0.1 s of load to reach its steady clock).
+  * "dist_us": p10 / p50 / p90 over max(steps, 100) calls, each between its
+    own pair of events (rotating sets).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1,c3] [--no-cpu] [--no-hot]
 """
 import argparse
 import json
+import math
 import os
+import platform
 import sys
 import time
 
@@ -23,20 +40,39 @@ PEAK_F32_MFMA = 157.3e12   # MI355X dense fp32 matrix, FLOP/s
 PEAK_BF16_MFMA = 2.5e15    # dense bf16 matrix
 PEAK_HBM = 8.0e12          # HBM3E bytes/s
 METRIC = "causal attention fwd TFLOP/s + % of MFMA roofline on 1 MI355X (B32 H8 S256 D32)"
+ROTATE_BYTES = 1 << 30     # buffer sets per config hold at least this much together
+SEED = 0x48495047
 
 # name: (B, H, Sq, Sk, D, causal, dtype, probs, kind)
+# "legacy" lines are the drop-in call HipGPT makes (src/transformer_layer.cpp:
+# 208, 218-219): non-causal, probs written, through launch_multihead_attention
+# on the null stream.  "probs" lines are causal with probs (extended API).
 CONFIGS = {
     "c1": (32, 8, 256, 256, 32, True, "f32", False, "fwd"),
     "c1_probs": (32, 8, 256, 256, 32, True, "f32", True, "fwd"),
     "c1_legacy": (32, 8, 256, 256, 32, False, "f32", True, "fwd"),
     "c2": (32, 8, 256, 256, 64, True, "f32", False, "fwd"),
     "c2_probs": (32, 8, 256, 256, 64, True, "f32", True, "fwd"),
+    "c2_legacy": (32, 8, 256, 256, 64, False, "f32", True, "fwd"),
     "c3": (8, 12, 1024, 1024, 64, True, "f32", False, "fwd"),
+    "c3_probs": (8, 12, 1024, 1024, 64, True, "f32", True, "fwd"),
+    "c3_legacy": (8, 12, 1024, 1024, 64, False, "f32", True, "fwd"),
     "c3_bf16": (8, 12, 1024, 1024, 64, True, "bf16", False, "fwd"),
     "c4": (4, 16, 2048, 2048, 128, True, "f32", False, "fwd"),
+    "c4_probs": (4, 16, 2048, 2048, 128, True, "f32", True, "fwd"),
+    "c4_legacy": (4, 16, 2048, 2048, 128, False, "f32", True, "fwd"),
     "c5": (64, 12, 1, 2048, 64, False, "f32", False, "decode"),
     # c5 as a KV-cache step: 2047 cached rows + the new one appended in place
     "c5_kvcache": (64, 12, 1, 2048, 64, False, "f32", False, "kvcache"),
+    # One long sequence: few (b, h) rows, so the keys are split over 32
+    # workgroups per row and the reduce kernel merges them.
+    "decode_long": (1, 12, 1, 32768, 64, False, "f32", False, "decode"),
+    # The c1 head shape at other batch sizes: HipGPT's generation call
+    # (GPTModel::generate, src/gpt_model.cpp:273: B = 1, non-causal, probs)
+    # and a batch whose grid is four times the device's resident slots.
+    "gen_b1_legacy": (1, 8, 256, 256, 32, False, "f32", True, "fwd"),
+    "c1_b128": (128, 8, 256, 256, 32, True, "f32", False, "fwd"),
+    "c1_b128_legacy": (128, 8, 256, 256, 32, False, "f32", True, "fwd"),
     # HipGPT's unfused single-head helpers (include/hip_kernels.h:44-46) at the
     # c1 shape with batch and heads merged (B*H = 256 sequences of 256 x 32).
     "a8_scores": (256, 1, 256, 256, 32, False, "f32", False, "sdp"),
@@ -108,10 +144,31 @@ def work(cfg):
     return flops, nbytes
 
 
-def make_call(cfg, torch, A, dev):
+def set_bytes(cfg):
+    """Device bytes of one input + output set of a config (for the rotation count)."""
+    B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
+    if kind == "gemm":
+        M, N, K = B, H, Sq
+        return 4 * (M * K + K * N + N + M * N)
+    if kind in ("sdp", "softmax", "wsum"):
+        return 4 * (3 * B * Sq * D + 2 * B * Sq * Sk + B * Sq * D)
+    E = H * D
+    if kind == "bwd":
+        return 4 * (3 * B * Sq * E + B * Sq * E + B * Sq * E + B * H * Sq * Sk + 3 * B * Sq * E)
+    if kind in ("fwd_lse", "bwd_lse"):
+        return 4 * (3 * B * Sq * E + 2 * B * Sq * E + B * H * Sq + 3 * B * Sq * E)
+    if kind in ("decode", "kvcache"):
+        return 4 * B * H * D * (2 * Sk + 4)
+    el = 2 if dtype == "bf16" else 4
+    return el * B * H * D * (Sq + 2 * Sk) + 4 * B * H * Sq * D + (4 * B * H * Sq * Sk if probs else 0)
+
+
+def make_call(cfg, torch, A, dev, seed=SEED):
+    """One input/output set of a config and the call that runs it.
+    Returns (fn, extra)."""
     B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
     g = torch.Generator(device=dev)
-    g.manual_seed(0x48495047)
+    g.manual_seed(seed)
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     if kind == "decode":
         q = torch.randn(B, 1, H, D, device=dev, generator=g)
@@ -120,7 +177,8 @@ def make_call(cfg, torch, A, dev):
         out = torch.empty(B, 1, H, D, device=dev)
         ns = A.decode_default_splits(B, H, Sk)
         ws = torch.empty(max(1, A.decode_workspace_bytes(B, H, D, ns) // 4), device=dev)
-        return lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws), {"splits": ns}
+        return (lambda: A.decode(q, k, v, out=out, num_splits=ns, workspace=ws),
+                {"splits": ns, "entry": "hipgpt_attn_decode"})
     if kind == "kvcache":
         kc = torch.randn(B, Sk, H, D, device=dev, generator=g)
         vc = torch.randn(B, Sk, H, D, device=dev, generator=g)
@@ -184,62 +242,147 @@ def make_call(cfg, torch, A, dev):
         qkv = torch.randn(3 * B * Sq * E, device=dev, generator=g)
         out = torch.empty(B * Sq, E, device=dev)
         p = torch.empty(B, H, Sq, Sk, device=dev) if probs else None
-        return lambda: A.qkv_planar(qkv, out, p, B, Sq, E, H, causal=causal), {"layout": "planar [3][B*S][E]"}
+        if probs and not causal:  # the drop-in symbol, exactly as HipGPT calls it
+            return (lambda: A.launch_multihead_attention(qkv, out, p, B, Sq, E, H),
+                    {"layout": "planar [3][B*S][E]", "entry": "launch_multihead_attention (null stream)"})
+        return (lambda: A.qkv_planar(qkv, out, p, B, Sq, E, H, causal=causal),
+                {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_qkv_planar"})
     q = torch.randn(B, Sq, H, D, device=dev, generator=g).to(tdt)
     k = torch.randn(B, Sk, H, D, device=dev, generator=g).to(tdt)
     v = torch.randn(B, Sk, H, D, device=dev, generator=g).to(tdt)
     out = torch.empty(B, Sq, H, D, device=dev)
     p = torch.empty(B, H, Sq, Sk, device=dev) if probs else None
-    return lambda: A.attention(q, k, v, out=out, probs=p, causal=causal), {"layout": "[B,S,H,D]"}
+    return (lambda: A.attention(q, k, v, out=out, probs=p, causal=causal),
+            {"layout": "[B,S,H,D]", "entry": "hipgpt_attn_fwd"})
 
 
-def time_call(fn, steps, warmup, torch, min_warm_s=0.2):
-    """ms per call over exactly `steps` back-to-back calls, HIP events on the
-    stream the calls launch on.  The untimed warm-up is `warmup` calls and at
-    least `min_warm_s` seconds of calls right before the timed region: the
-    MI355X needs ~0.1 s of load to reach its steady clock, and an idle gap
-    before the timed calls (allocation, another config's set-up) would
-    otherwise be timed at the lower clock."""
+def warm_up(fns, warmup, torch, min_warm_s=0.2):
+    """`warmup` calls and at least `min_warm_s` seconds of calls, rotating over
+    the sets: the MI355X needs ~0.1 s of load to reach its steady clock, and
+    an idle gap right before the timed calls would be timed at a lower clock."""
     n = 0
     t_end = time.perf_counter() + min_warm_s
     while n < warmup or time.perf_counter() < t_end:
-        fn()
+        fns[n % len(fns)]()
         n += 1
         if n % 50 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()  # the stream the library launches on
+
+
+def time_call(fns, steps, warmup, torch):
+    """ms per call over exactly `steps` back-to-back calls (call i on set
+    i % len(fns)), HIP events on the stream the calls launch on."""
+    warm_up(fns, warmup, torch)
+    stream = torch.cuda.current_stream()  # the stream the library launches on (the null stream here)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fns[i % len(fns)]()
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps  # ms per call
+    return start.elapsed_time(stop) / steps
 
 
-def cpu_baseline(nthreads, min_seconds=10.0):
-    """The oracle's scalar restatement of the reference kernel HipGPT runs for
-    c1 (flash_attention_kernel<32>, causal-restricted) on the whole c1
-    problem, on the host cores; repeated until min_seconds have elapsed,
-    median time reported."""
+def launch_dist(fns, n, torch):
+    """Per-call times (us) of n calls, each between its own pair of events;
+    returns p10 / p50 / p90."""
+    import numpy as np
+
+    warm_up(fns, 0, torch)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record(stream)
+        fns[i % len(fns)]()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t = np.array([a.elapsed_time(b) * 1e3 for a, b in ev])
+    p10, p50, p90 = np.percentile(t, [10, 50, 90])
+    return {"p10": round(float(p10), 3), "p50": round(float(p50), 3), "p90": round(float(p90), 3), "n": n}
+
+
+# ------------------------------------------------------------ CPU baseline
+
+CPU_CONFIGS = ("c1", "c2", "c3", "c4", "c5")
+
+
+def host_info():
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": affinity}
+
+
+def cpu_config(name, nthreads, budget_s):
+    """The oracle's scalar restatement of the reference kernel HipGPT would run
+    for config `name` (flash_attention_kernel passes for D in {32, 64} with
+    S <= 512, the fallback's three-pass recompute otherwise; causal configs
+    restricted to keys j <= i; c5 = the last row of the S = 2048 fallback,
+    i.e. one query against 2048 keys) on the host cores.  Every (b, h) pair
+    costs the same, so a subsample of evenly spaced pairs is timed and scaled
+    by B*H / pairs: the pair count doubles from `nthreads` until one run takes
+    at least budget_s / 3 (or covers every pair), then runs repeat until
+    budget_s / 2 has elapsed; the median run is reported."""
     import statistics
 
     import oracle as O
 
-    B, H, S, D = 32, 8, 256, 32
-    E = H * D
-    qkv = O.seeded_planar(0x48495047, B, S, E)
-    q, k, v = O.planar_qkv(qkv, B, S, E, H)
-    times = []
-    while sum(times) < min_seconds or len(times) < 3:
+    B, H, Sq, Sk, D, causal, dtype, probs, kind = CONFIGS[name]
+    variant = O.FLASH if (kind == "fwd" and D in (32, 64) and Sk <= 512) else O.FALLBACK
+    q, k, v = O.seeded_bshd(SEED, B, Sq, Sk, H, D)
+    allp = [(b, h) for b in range(B) for h in range(H)]
+
+    def pick(n):
+        step = len(allp) / n
+        return [allp[int(i * step)] for i in range(n)]
+
+    def run(n):
+        pr = pick(n)
         t0 = time.perf_counter()
-        O.attention(q, k, v, causal=True, variant=O.FLASH, nthreads=nthreads)
-        times.append(time.perf_counter() - t0)
+        O.attention(q, k, v, causal=causal, variant=variant, nthreads=nthreads, pairs=pr)
+        return time.perf_counter() - t0
+
+    n = min(nthreads, len(allp))
+    dt = run(n)
+    while dt < budget_s / 3 and n < len(allp):
+        n = min(2 * n, len(allp))
+        dt = run(n)
+    times = [dt]
+    while sum(times) < budget_s / 2:
+        times.append(run(n))
     dt = statistics.median(times)
-    flops, _ = work(CONFIGS["c1"])
-    return flops / dt, dt, len(times)
+    flops, _ = work(CONFIGS[name])
+    us = dt * len(allp) / n * 1e6
+    return {"us_per_call": round(us, 1), "gflops": round(flops / (us * 1e-6) / 1e9, 3), "threads": nthreads,
+            "pairs": n, "of_pairs": len(allp), "runs": len(times),
+            "variant": "flash" if variant == O.FLASH else "fallback"}
+
+
+def cpu_baseline(budget_1t=3.0, budget_all=1.5):
+    """c1..c5 at 1 thread and at all usable host cores (the box's CPU share
+    for one GPU is 16 threads, whatever nproc reports)."""
+    info = host_info()
+    ncores = max(1, min(16, info["affinity"]))
+    cfgs = {}
+    for name in CPU_CONFIGS:
+        one = cpu_config(name, 1, budget_1t)
+        alln = cpu_config(name, ncores, budget_all)
+        cfgs[name] = {"one_thread": one, "all_cores": alln}
+        print(f"# cpu {name}: 1 thread {one['us_per_call']:.0f} us ({one['pairs']}/{one['of_pairs']} pairs), "
+              f"{ncores} threads {alln['us_per_call']:.0f} us", file=sys.stderr, flush=True)
+    return info, ncores, cfgs
 
 
 def read_traffic(name):
@@ -257,6 +400,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated config names (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the host baseline")
+    ap.add_argument("--no-hot", action="store_true", help="skip the one-set (cache-hot) timing")
+    ap.add_argument("--no-dist", action="store_true", help="skip the per-call distribution")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run one plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -273,6 +418,9 @@ def main():
 
     dev = torch.device("cuda:0")
     names = [n for n in args.only.split(",") if n] or list(CONFIGS)
+    unknown = [n for n in names if n not in CONFIGS]
+    if unknown:
+        sys.exit(f"bench.py: unknown config(s) {unknown}")
     results = {}
     # Bring the GPU to its steady clock before the first timed config.
     fn0, _ = make_call(CONFIGS[names[0]], torch, A, dev)
@@ -284,34 +432,42 @@ def main():
     del fn0
     for name in names:
         cfg = CONFIGS[name]
+        nsets = max(1, math.ceil(ROTATE_BYTES / set_bytes(cfg)))
         try:
-            fn, extra = make_call(cfg, torch, A, dev)
+            sets = [make_call(cfg, torch, A, dev, seed=SEED + i) for i in range(nsets)]
         except Exception as e:  # e.g. a dtype this build has no kernel for
             results[name] = {"error": str(e)}
             continue
+        fns = [f for f, _ in sets]
+        extra = sets[0][1]
         try:
-            ms = time_call(fn, args.steps, args.warmup, torch)
+            ms = time_call(fns, args.steps, args.warmup, torch)
+            ms_hot = None if args.no_hot else time_call(fns[:1], args.steps, args.warmup, torch)
+            dist = None if args.no_dist else launch_dist(fns, max(args.steps, 100), torch)
         except Exception as e:
             results[name] = {"error": str(e)}
             continue
+        del sets, fns
         flops, nbytes = work(cfg)
         B, H, Sq, Sk, D, causal, dtype, probs, kind = cfg
         peak = PEAK_BF16_MFMA if dtype == "bf16" else PEAK_F32_MFMA
         t_mfma = flops / peak
         t_hbm = nbytes / PEAK_HBM
         bound = "hbm" if t_hbm > t_mfma else "mfma"
-        # the null stream the helpers launch on is torch's default stream here
         tflops = flops / (ms * 1e-3) / 1e12
         gbs = nbytes / (ms * 1e-3) / 1e9
         frac = (t_hbm if bound == "hbm" else t_mfma) / (ms * 1e-3)
         results[name] = {
             "shape": {"B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D}, "causal": causal,
             "dtype": dtype, "probs": probs, "us_per_call": round(ms * 1e3, 3),
-            "tflops": round(tflops, 3), "gbs": round(gbs, 1), "bound": bound,
+            "us_per_call_hot": None if ms_hot is None else round(ms_hot * 1e3, 3), "dist_us": dist,
+            "sets": nsets, "tflops": round(tflops, 3), "gbs": round(gbs, 1), "bound": bound,
             "roofline_frac": round(frac, 4), **extra,
         }
-        print(f"# {name}: {ms * 1e3:.2f} us  {tflops:.2f} TFLOP/s  {gbs:.0f} GB/s  "
-              f"{bound}-bound frac {frac:.3f}", file=sys.stderr, flush=True)
+        hot = "" if ms_hot is None else f" (hot {ms_hot * 1e3:.2f})"
+        print(f"# {name}: {ms * 1e3:.2f} us{hot}  {tflops:.2f} TFLOP/s  {gbs:.0f} GB/s  "
+              f"{bound}-bound frac {frac:.3f}  sets {nsets}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
 
     if args.copy_mb > 0:
         # A plain copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counters.
@@ -336,7 +492,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic N(0,1) Q/K/V resident in HBM (planar [3][B*S][E] buffer, seeded)",
+        "data": "synthetic N(0,1) Q/K/V resident in HBM (planar [3][B*S][E] buffer, seeded; calls rotate "
+                "over buffer sets totalling >= 1 GiB so operands come from HBM, not the Infinity Cache)",
         "config": {"workload": "c1: causal self-attention forward, fp32, B=32 H=8 S=256 D=32 (E=256), "
                                "no probs output", "B": 32, "H": 8, "S": 256, "D": 32,
                    "parallelism": "single GPU"},
@@ -349,14 +506,18 @@ def main():
             "unit": "TFLOP/s", "frac": round(ach / PEAK_F32_MFMA, 4), "traffic": read_traffic("c1"),
         }
     if not args.no_cpu:
-        cpu1, dt1, n1 = cpu_baseline(1)
-        ncores = min(16, os.cpu_count() or 1)
-        cpun, dtn, _ = cpu_baseline(ncores, min_seconds=2.0)
+        info, ncores, cfgs = cpu_baseline()
+        c1 = cfgs["c1"]["one_thread"]
         line["cpu_baseline"] = {
-            "value": round(cpu1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"whole c1 problem (causal, 256 (b,h) pairs) through the scalar restatement of "
-                      f"flash_attention_kernel<32>: median {dt1:.3f} s of {n1} runs on 1 thread",
-            "all_cores": {"value": round(cpun / 1e12, 6), "cores": ncores, "seconds": round(dtn, 3)},
+            "value": round(c1["gflops"] / 1e3, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"c1 (causal) through the oracle's scalar restatement of flash_attention_kernel<32>: "
+                      f"{c1['pairs']} of {c1['of_pairs']} (b,h) pairs, median of {c1['runs']} runs on 1 thread, "
+                      f"{c1['us_per_call']:.0f} us per c1 call; c2..c5 in 'configs' (subsampled pairs scaled "
+                      f"by B*H/pairs; c3/c4/c5 the fallback's 3-pass math)",
+            "host": info,
+            "all_cores": {"value": round(cfgs["c1"]["all_cores"]["gflops"] / 1e3, 6), "cores": ncores,
+                          "us_per_call": cfgs["c1"]["all_cores"]["us_per_call"]},
+            "configs": cfgs,
         }
     line["configs"] = results
     print(json.dumps(line), flush=True)

@@ -61,6 +61,7 @@ SIGNATURES = {
     "hipgpt_gemm_bias": (
         _int, [_vp, _vp, _vp, _vp, _int, _int, _int, _i64, _i64, _i64, _int, _i64, _int, _vp]),
     "hipgpt_qkv_projection": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _vp]),
+    "hipgpt_attn_wait_expired": (_int, [ctypes.POINTER(ctypes.c_uint), _int]),
     "hipgpt_attn_decode_default_splits": (_int, [_int, _int, _int]),
     "hipgpt_attn_decode_workspace_bytes": (ctypes.c_size_t, [_int, _int, _int, _int]),
     "hipgpt_attn_decode": (
@@ -116,6 +117,14 @@ def lib() -> ctypes.CDLL:
             cxx.argtypes = SIGNATURES["hipgpt_launch_multihead_attention"][1]
             _lib = handle
     return _lib
+
+
+def wait_expired(clear: bool = True) -> int:
+    """Bounded LDS-flag waits that ran out on the current device since the
+    last clear (hipgpt_attn_wait_expired); zero in a correct run."""
+    n = ctypes.c_uint(0)
+    check(lib().hipgpt_attn_wait_expired(ctypes.byref(n), 1 if clear else 0), "hipgpt_attn_wait_expired")
+    return int(n.value)
 
 
 def check(status: int, what: str = "") -> None:

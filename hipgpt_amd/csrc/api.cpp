@@ -438,6 +438,15 @@ int hipgpt_attn_decode_kvcache(const float* q, const float* k_new, const float* 
     return from_hip(hipgpt::launch_decode(a, hipgpt::kF32, ns, static_cast<float*>(workspace), stream, &kc));
 }
 
+int hipgpt_attn_wait_expired(unsigned int* count, int clear) {
+    if (!count) return HIPGPT_ERR_INVALID;
+    unsigned int fwd = 0, bwd = 0;
+    if (hipgpt::fa_f32_wait_expired(&fwd, clear != 0) != hipSuccess) return HIPGPT_ERR_LAUNCH;
+    if (hipgpt::bwd_wait_expired(&bwd, clear != 0) != hipSuccess) return HIPGPT_ERR_LAUNCH;
+    *count = fwd + bwd;
+    return HIPGPT_OK;
+}
+
 void hipgpt_launch_matmul(const float* A, const float* B, float* C, int M, int N, int K) {
     launch_matmul(A, B, C, M, N, K);
 }

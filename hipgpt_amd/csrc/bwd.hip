@@ -321,6 +321,8 @@ hipError_t launch_dp(const BwdArgs& a, hipStream_t s) {
 #define HIPGPT_BWDKV_NQS 1
 #endif
 
+hipError_t bwd_wait_expired(unsigned int* count, bool clear) { return wait_expired_take(count, clear); }
+
 bool bwd_tiled_ok(const BwdArgs& a) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     return (a.D == 32 || a.D == 64) && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) && al(a.k) &&

@@ -87,12 +87,14 @@ __host__ __device__ constexpr Layout layout(int Sp) {
 constexpr int kMaxLdsBytes = layout(MAXS).total * 4;
 
 // Wait until *flag >= v (another wave of the workgroup stores it with
-// release order), for at most kSpinMax polls.
+// release order), for at most kSpinMax polls; an expiry is counted
+// (note_wait_expired) for the host to see.
 __device__ __forceinline__ void wait_ge(const int* flag, int v) {
     for (int n = 0; n < kSpinMax; ++n) {
         if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return;
         __builtin_amdgcn_s_sleep(1);
     }
+    if ((threadIdx.x & 63) == 0) note_wait_expired();
 }
 __device__ __forceinline__ void set_flag(int* flag, int v) {
     __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -148,10 +150,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // one key tile's rows for every resident workgroup, at ~6 TB/s) lets the
     // early key tiles' rows arrive first instead of every wave waiting for all
     // of them.  s_memrealtime counts 10 ns; the wait is at most 7 slots.
-    if (!PROBS && CAUSAL && kt > 0) {
+    // Only the first set of workgroups, which the device starts together,
+    // loads in a burst; later ones start as slots free up and are not delayed.
+    if (!PROBS && CAUSAL && kt > 0 && bhi < a.resident) {
         constexpr int kWaveBytes = 5 * BK * D * 4;  // Q, dO, O rows + K, V rows
-        const int resident = gridDim.x < 256u ? (int)gridDim.x : 256;
-        const unsigned long long slot = (unsigned long long)resident * kWaveBytes / HIPGPT_BH_SLOT_DIV;
+        const unsigned long long slot = (unsigned long long)a.resident * kWaveBytes / HIPGPT_BH_SLOT_DIV;
         const unsigned long long until = t_start + slot * kt;
         for (int n = 0; n < 4096 && __builtin_amdgcn_s_memrealtime() < until; ++n) __builtin_amdgcn_s_sleep(2);
     }
@@ -333,12 +336,24 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 
     // Stored probs, phase 2: P of query tile i in the accumulator's order
     // (register r <-> query i*32 + acc_key(r, h), lane <-> key kj); keys
-    // past S read as zero through an out-of-range offset.
+    // past S read as zero through an out-of-range offset.  The buffer range
+    // check covers the vector offset (and the immediate) only, never the
+    // scalar offset: a whole tile in range puts each register's row offset in
+    // the scalar operand, the last tile of a ragged S (rows past S) folds it
+    // into the vector offset so those rows read as zero.
     auto load_pk = [&](floatx16& pv, int i) {
         const int vo = kval ? (i * BK + 4 * hf) * S4 + kj * 4 : 0x40000000;
+        if (i * BK + BK <= S) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            pv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, vo, (8 * (r >> 2) + (r & 3)) * S4, 0));
+            for (int r = 0; r < 16; ++r)
+                pv[r] = __builtin_bit_cast(float,
+                                           __builtin_amdgcn_raw_buffer_load_b32(pr, vo, (8 * (r >> 2) + (r & 3)) * S4, 0));
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                pv[r] = __builtin_bit_cast(float,
+                                           __builtin_amdgcn_raw_buffer_load_b32(pr, vo + (8 * (r >> 2) + (r & 3)) * S4, 0, 0));
+        }
     };
     floatx16 pnext;
     if constexpr (PROBS) load_pk(pnext, kt);
@@ -357,8 +372,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
         return aq;
     };
-    // dQ rows through a buffer resource ending at row S-1: stores past it are
-    // dropped, and each register's row offset is a scalar.
+    // dQ rows through a buffer resource ending at row S-1.  As for the P
+    // loads, only the vector offset is range-checked: whole tiles use a scalar
+    // row offset per register, the last tile of a ragged S puts it in the
+    // vector offset so the stores of rows past S are dropped.
     const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(
         a.dq + base, 0, (int)(((int64_t)(S - 1) * a.ts + D) * 4), kBufferFlags);
     const int row4 = a.ts * 4;
@@ -374,10 +391,17 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         }
         if (t == nc - 1) {
             const int vo = (i * BK + 4 * hf) * row4 + c * 4;
+            if (i * BK + BK <= S) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr, vo,
-                                                      (8 * (r >> 2) + (r & 3)) * row4, 0);
+                for (int r = 0; r < 16; ++r)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr, vo,
+                                                          (8 * (r >> 2) + (r & 3)) * row4, 0);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr,
+                                                          vo + (8 * (r >> 2) + (r & 3)) * row4, 0, 0);
+            }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) part[(8 * (r >> 2) + (r & 3)) * PP] = aq[r];
@@ -504,7 +528,12 @@ hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
         attr_set.fetch_or(bit, std::memory_order_release);
     }
     const int Sp = (a.S + BK - 1) / BK * BK;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bh::NW * 64), (size_t)bh::layout(Sp).total * 4, s, a);
+    const size_t lds = (size_t)bh::layout(Sp).total * 4;
+    BwdArgs args = a;
+    static ResidentSlots cache[bh::NW];  // per LDS footprint: Sp / 32 - 1
+    const int slots = cache[Sp / BK - 1].get(reinterpret_cast<const void*>(kern), bh::NW * 64, lds);
+    args.resident = (int)(grid < slots ? grid : slots);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bh::NW * 64), lds, s, args);
     return hipGetLastError();
 }
 

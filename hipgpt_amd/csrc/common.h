@@ -46,6 +46,10 @@ struct AttnArgs {
     float qscale;    // softmax scale * log2(e), folded into Q
     int n_qblk;      // query blocks per (b,h)
     float* lse;      // optional [B*H][Sq]: ln sum_j exp(scale * q_i . k_j) over visible keys
+    // Start stagger (set by the launcher): workgroups [0, stagger_slots) --
+    // the first set the device holds at once -- delay their first loads by
+    // their launch rank; 0 = no stagger.
+    int stagger_slots;
 };
 
 // exp2 on the transcendental unit (v_exp_f32): exp2(-inf) = 0.
@@ -64,6 +68,58 @@ __device__ __forceinline__ float wave_sum(float x) {
     for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
     return x;
 }
+
+// Bounded waits.  Kernels whose waves wait on LDS flags set by other waves of
+// the workgroup (instead of a barrier) poll a bounded number of times, so a
+// schedule mistake cannot hang the GPU.  A wait that runs out lets the wave go
+// on with data that may never have been published; each such expiry is counted
+// here (one counter per translation unit and device, a vector atomic) and the
+// host reads the count through wait_expired_take().
+static __device__ unsigned int g_wait_expired;
+
+__device__ __forceinline__ void note_wait_expired() {
+    __hip_atomic_fetch_add(&g_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Host: this translation unit's expiry count on the current device (blocking
+// copy on the null stream), cleared when `clear` is set and it was non-zero.
+static inline hipError_t wait_expired_take(unsigned int* count, bool clear) {
+    hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_wait_expired), sizeof(unsigned int), 0,
+                                       hipMemcpyDeviceToHost);
+    if (e == hipSuccess && clear && *count != 0) {
+        const unsigned int zero = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_expired), &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
+    }
+    return e;
+}
+
+// Workgroups of kernel `kern` (block threads, dynamic LDS bytes) the current
+// device holds at once: occupancy per CU times the CU count; 0 if unknown.
+// The caller caches the value per device and kernel (static state of its own
+// template instantiation).
+inline int device_resident_slots(const void* kern, int block, size_t lds) {
+    int dev = 0, per_cu = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, block, lds) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    return per_cu > 0 && cus > 0 ? per_cu * cus : 0;
+}
+
+// Per-device cache of device_resident_slots for one kernel (a static of the
+// launching template, so each kernel instantiation has its own).
+struct ResidentSlots {
+    int slots[64] = {};
+    int get(const void* kern, int block, size_t lds) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+        int v = __atomic_load_n(&slots[dev], __ATOMIC_RELAXED);
+        if (v == 0) {
+            v = device_resident_slots(kern, block, lds);
+            __atomic_store_n(&slots[dev], v, __ATOMIC_RELAXED);
+        }
+        return v;
+    }
+};
 
 // Workgroups are dispatched to the 8 XCDs round-robin (id % 8), and each XCD
 // has its own L2.  xcd_remap renumbers a 1-D grid so that XCD x runs the

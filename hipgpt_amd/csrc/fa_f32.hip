@@ -194,6 +194,8 @@ hipError_t launch_dp(const AttnArgs& a, bool causal, bool probs, bool vec, hipSt
 
 }  // namespace
 
+hipError_t fa_f32_wait_expired(unsigned int* count, bool clear) { return wait_expired_take(count, clear); }
+
 int fa_f32_padded_dim(int D) {
     if (D <= 32) return 32;
     if (D <= 64) return 64;

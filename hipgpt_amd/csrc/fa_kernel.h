@@ -32,7 +32,8 @@ namespace fa {
 
 // Start stagger of short causal grids (see FaKernel::run): 35 ticks of the
 // 100 MHz s_memrealtime counter = 350 ns per launch rank, for grids of at
-// most 4 query blocks per (batch, head) (c1: 16.1 -> 15.8 us against 200 ns;
+// most 4 query blocks per (batch, head) that fill at least half of the
+// device's resident workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
 // measured over 100 .. 800 ns per rank).
 constexpr unsigned long long kStaggerTicks = 35;
 // The same for grids that write probs: 1 us per rank without a causal mask
@@ -195,7 +196,7 @@ struct FaKernel {
         const E* Vp = static_cast<const E*>(a.v) + b * a.v_bs + h * a.v_hs;
 
         // Short causal problems (a few query blocks per (batch, head), the
-        // whole grid resident at once) start with every workgroup loading its
+        // grid filling the device's resident slots) start with every workgroup loading its
         // first stage at the same moment, and the first tile computes only
         // when that burst has drained.  Launch rank r waits r * 350 ns first,
         // so the longest query blocks (rank 0) get their operands earliest
@@ -203,7 +204,11 @@ struct FaKernel {
         // Writing probs, the ranks are spread further apart, so one rank's
         // probs stores (the second sweep, HBM-bound) overlap the next rank's
         // score sweep (MFMA-bound) instead of every workgroup storing at once.
-        if ((CAUSAL || PROBS) && a.n_qblk <= kStaggerMaxBlocks && rank > 0) {
+        // Only the workgroups the device starts together (block ids below
+        // stagger_slots, set by the launcher when the grid fills at least half
+        // of the resident slots) are delayed: a small grid has no burst to
+        // spread, and later workgroups of a large grid start as slots free up.
+        if ((CAUSAL || PROBS) && rank > 0 && (int)blockIdx.x < a.stagger_slots) {
             const unsigned long long ticks = PROBS ? (CAUSAL ? kStaggerTicksProbsCausal : kStaggerTicksProbs) : kStaggerTicks;
             const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)rank * ticks;
             for (int i = 0; i < 1024 && __builtin_amdgcn_s_memrealtime() < t_end; ++i) __builtin_amdgcn_s_sleep(2);
@@ -512,8 +517,14 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     args.n_qblk = (a.Sq + NQS * QW - 1) / (NQS * QW);
     const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>), dim3((unsigned)grid),
-                       dim3(NQS * NKS * 64), 0, stream, args);
+    auto kern = fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>;
+    args.stagger_slots = 0;
+    if ((CAUSAL || PROBS) && args.n_qblk > 1 && args.n_qblk <= kStaggerMaxBlocks) {
+        static ResidentSlots cache;
+        const int slots = cache.get(reinterpret_cast<const void*>(kern), NQS * NKS * 64, 0);
+        if (slots > 0 && 2 * grid >= slots) args.stagger_slots = slots;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), 0, stream, args);
     return hipGetLastError();
 }
 

@@ -146,11 +146,13 @@ struct FaResident {
             if (lane == 0) __hip_atomic_fetch_add(&cnt[t], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         };
         auto wait_tile = [&](int t) {
-            // Bounded: every wave signals every tile before waiting on it.
+            // Bounded: every wave signals every tile before waiting on it.  An
+            // expiry is counted (note_wait_expired) for the host to see.
             for (int spin = 0; spin < (1 << 22); ++spin) {
-                if (__hip_atomic_load(&cnt[t], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW) break;
+                if (__hip_atomic_load(&cnt[t], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW) return;
                 __builtin_amdgcn_s_sleep(1);
             }
+            if (lane == 0) note_wait_expired();
         };
 
         // ---- consumer state ----

@@ -21,6 +21,12 @@ hipError_t launch_fa_bf16(const AttnArgs& a, bool causal, hipStream_t stream);
 // Any head dim, fp32: one wave per query row (the path for D > 128).
 hipError_t launch_attn_generic_f32(const AttnArgs& a, bool causal, hipStream_t stream);
 
+// Expired bounded waits (note_wait_expired) of the kernels in fa_f32.hip (the
+// resident-K/V forward) and bwd.hip (the per-(b, h) backward) on the current
+// device; cleared after the read when `clear` is set.
+hipError_t fa_f32_wait_expired(unsigned int* count, bool clear);
+hipError_t bwd_wait_expired(unsigned int* count, bool clear);
+
 // KV-cache decode step: the cache is a.k / a.v (with a.k_* / a.v_* strides,
 // a.Sk = max_len); the new row of sequence b is appended at lens[b].
 struct KvcArgs {
@@ -57,6 +63,10 @@ struct BwdArgs {
     int B, H, S, D;
     int causal;
     float scale;
+    // Set by the launcher: workgroups the device holds at once for the chosen
+    // kernel, capped at the grid (0 = unknown); the per-(b, h) kernel's
+    // staggered start is timed for, and applied to, that first set.
+    int resident;
 };
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s);
 // The LDS-tiled MFMA kernels apply (D = 32 or 64, 16-byte aligned rows); the

@@ -157,6 +157,16 @@ int hipgpt_attn_decode_kvcache(const float* q, const float* k_new,
                                int num_splits, int advance, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
 
+/* Diagnostics, no counterpart in HipGPT.  Two kernels synchronise their waves
+ * through LDS flags instead of barriers (the resident-K/V forward at D = 64,
+ * S <= 256, and the one-workgroup-per-(b, h) backward at D = 32, S <= 256).
+ * Their waits are bounded so a fault in the schedule cannot hang the GPU; a
+ * wait that runs out is counted on the device.  *count receives the number
+ * of expired waits on the current device since the last clear (zero in a
+ * correct run; non-zero means some outputs may be wrong).  clear != 0 resets
+ * the count.  Blocking: a copy on the null stream. */
+int hipgpt_attn_wait_expired(unsigned int* count, int clear);
+
 /* ---- projections either side of the attention (fp32 MFMA GEMM) ---- */
 
 /* C-linkage twins of launch_matmul / launch_matmul_add_bias

@@ -157,3 +157,39 @@ def test_baseline_config_backward(dev, cfg):
     A.attention_backward(dev_t(go), dev_t(qkv), dev_t(probs), d_g, B, S, E, H, causal=True, workspace=ws)
     got = host(d_g)
     assert np.abs(got - want).max() <= tol(want)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,S,E,H", [(2, 44, 64, 2), (3, 100, 128, 4), (2, 236, 64, 2)])
+def test_per_bh_backward_ragged_tail_stays_in_bounds(dev, B, S, E, H, causal):
+    """D = 32 with S % 32 != 0 (S % 4 == 0) runs the one-workgroup-per-(b, h)
+    kernel with a partial last tile, in both modes.  NaN sits directly after
+    the probs inside the same allocation, so a P load past the last (b, h)'s
+    row S-1 would poison dK / dV; rows past S of one (b, h)'s dQ are the next
+    batch's rows (or the dK plane), so a dQ store past S would overwrite
+    gradients.  Every element must be finite and match the oracle."""
+    qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=13)
+    want = O.mha_backward(go, qkv, probs, B, S, E, H)
+    n = probs.size
+    pbuf = torch.full((n + 64 * S,), float("nan"), device=dev)
+    pbuf[:n] = dev_t(probs.reshape(-1))
+    d_p = pbuf[:n]
+    d_qkv, d_go = dev_t(qkv), dev_t(go)
+    d_g = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    if causal:
+        ws = torch.empty(B * H * S, device=dev)
+        A.attention_backward(d_go, d_qkv, d_p, d_g, B, S, E, H, causal=True, workspace=ws)
+    else:
+        A.launch_multihead_attention_backward(d_go, d_qkv, d_p, d_g, B, S, E, H)
+    got = host(d_g)
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= tol(want)
+    # the probs-free pair on the same shape (its dQ stores take the same path)
+    out = torch.empty((B * S, E), device=dev)
+    lse = torch.empty(B * H * S, device=dev)
+    A.fwd_lse_qkv_planar(d_qkv, out, lse, B, S, E, H, causal=causal)
+    g2 = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    A.bwd_lse_qkv_planar(d_go, d_qkv, out, lse, g2, B, S, E, H, causal=causal)
+    got2 = host(g2)
+    assert np.isfinite(got2).all()
+    assert np.abs(got2 - want).max() <= tol(want)
