@@ -147,13 +147,21 @@ hipgpt::BwdArgs planar_bwd_args(const float* go, const float* qkv, const float* 
     return a;
 }
 
-float* cached_bwd_workspace(size_t bytes) {
+// Guards the cached workspace from the lookup until the kernels that use it
+// are enqueued, so a concurrent call that grows (frees) the buffer cannot
+// free it between another thread's lookup and launch.
+std::mutex& bwd_workspace_mutex() {
     static std::mutex mu;
+    return mu;
+}
+
+// Caller holds bwd_workspace_mutex().  Grows the current device's buffer when
+// too small (hipFree of the old one waits for the device to finish with it).
+float* cached_bwd_workspace(size_t bytes) {
     static void* buf[64] = {};
     static size_t cap[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
     if (cap[dev] < bytes) {
         if (buf[dev] && hipFree(buf[dev]) != hipSuccess) return nullptr;
         buf[dev] = nullptr;
@@ -174,12 +182,17 @@ void launch_multihead_attention_backward(const float* d_grad_attn_output, const 
     }
     if (B <= 0 || S <= 0 || E <= 0) return;
     hipgpt::BwdArgs a = planar_bwd_args(d_grad_attn_output, d_qkv, d_softmax, d_grad_qkv, B, S, E, H, 0);
-    if (hipgpt::bwd_uses_workspace(a)) {  // HipGPT's default shape (D = 32, S <= 256) needs none
-        a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
-        if (!a.dvec) {
-            fprintf(stderr, "launch_multihead_attention_backward: workspace allocation failed\n");
-            return;
-        }
+    if (!hipgpt::bwd_uses_workspace(a)) {  // HipGPT's default shape (D = 32, S <= 256) needs none
+        report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
+        return;
+    }
+    // Not capturable (it may allocate); hipgpt_attn_bwd_qkv_planar (caller
+    // workspace) is.
+    std::lock_guard<std::mutex> lock(bwd_workspace_mutex());
+    a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
+    if (!a.dvec) {
+        fprintf(stderr, "launch_multihead_attention_backward: workspace allocation failed\n");
+        return;
     }
     report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
 }
