@@ -19,6 +19,7 @@ ERR_INVALID = -1
 ERR_UNSUPPORTED = -2
 ERR_LAUNCH = -3
 ERR_WORKSPACE = -4
+ERR_SCRATCH = -5
 
 F32 = 0
 BF16 = 1
@@ -42,6 +43,7 @@ SIGNATURES = {
     "hipgpt_attn_bwd_workspace_bytes": (ctypes.c_size_t, [_int, _int, _int]),
     "hipgpt_attn_bwd_qkv_planar": (
         _int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, ctypes.c_size_t, _vp]),
+    "hipgpt_attn_bwd_qkv_planar_noalloc": (_int, [_vp, _vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_fwd_lse_qkv_planar": (_int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp]),
     "hipgpt_attn_bwd_lse_qkv_planar": (

@@ -187,7 +187,7 @@ void launch_multihead_attention_backward(const float* d_grad_attn_output, const 
         return;
     }
     // Not capturable (it may allocate); hipgpt_attn_bwd_qkv_planar (caller
-    // workspace) is.
+    // workspace) and hipgpt_attn_bwd_qkv_planar_noalloc are.
     std::lock_guard<std::mutex> lock(bwd_workspace_mutex());
     a.dvec = cached_bwd_workspace((size_t)B * H * S * sizeof(float));
     if (!a.dvec) {
@@ -196,6 +196,36 @@ void launch_multihead_attention_backward(const float* d_grad_attn_output, const 
     }
     report(hipgpt::launch_attn_bwd(a, 0), "launch_multihead_attention_backward");
 }
+
+// ------------------------------------------------- no-allocation backward
+// Fixed per-device scratch of hipgpt_attn_bwd_qkv_planar_noalloc: the B*H*S
+// row-dot workspace of the backward kernels (every element a call reads is
+// written earlier in the same call, so nothing needs clearing).  Each GPU the
+// library runs on holds its own copy until the process ends.  In host code
+// `scratch` names a host-side stand-in, never the device memory: its device
+// address comes from hipGetSymbolAddress, once per device (scratch_ptr).
+constexpr size_t kScratchFloats = (size_t)1 << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with it current) and kept per device.
+float* scratch_ptr() {
+    static std::mutex mu;
+    static float* ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        ptr[dev] = static_cast<float*>(p);
+    }
+    return ptr[dev];
+}
+
+}  // namespace
 
 // GEMMs either side of the attention (src/hip_kernels.cpp:102-154): the
 // reference's naming, A [M][N] x B [N][K] -> C [M][K].
@@ -242,6 +272,7 @@ const char* hipgpt_attn_strerror(int status) {
         case HIPGPT_ERR_UNSUPPORTED: return "unsupported problem (head dim, dtype or alignment)";
         case HIPGPT_ERR_LAUNCH: return "kernel launch failed";
         case HIPGPT_ERR_WORKSPACE: return "workspace missing or too small";
+        case HIPGPT_ERR_SCRATCH: return "problem exceeds the fixed scratch of the no-allocation entry point";
         default: return "unknown status";
     }
 }
@@ -283,6 +314,21 @@ int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv, const fl
     if (!workspace || workspace_bytes < hipgpt_attn_bwd_workspace_bytes(B, S, H)) return HIPGPT_ERR_WORKSPACE;
     hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, probs, grad_qkv, B, S, E, H, causal ? 1 : 0);
     a.dvec = static_cast<float*>(workspace);
+    return from_hip(hipgpt::launch_attn_bwd(a, stream));
+}
+
+int hipgpt_attn_bwd_qkv_planar_noalloc(const float* grad_out, const float* qkv, const float* probs,
+                                       float* grad_qkv, int B, int S, int E, int H, int causal,
+                                       hipStream_t stream) {
+    if (!grad_out || !qkv || !probs || !grad_qkv || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0)
+        return HIPGPT_ERR_INVALID;
+    if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
+    if ((uint64_t)B * (uint64_t)H * (uint64_t)S > kScratchFloats) return HIPGPT_ERR_SCRATCH;
+    hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, probs, grad_qkv, B, S, E, H, causal ? 1 : 0);
+    if (hipgpt::bwd_uses_workspace(a)) {
+        a.dvec = scratch_ptr();
+        if (!a.dvec) return HIPGPT_ERR_LAUNCH;
+    }
     return from_hip(hipgpt::launch_attn_bwd(a, stream));
 }
 

@@ -19,7 +19,8 @@ enum {
     HIPGPT_ERR_INVALID = -1,      /* bad size, stride, pointer or flag        */
     HIPGPT_ERR_UNSUPPORTED = -2,  /* valid problem this build has no kernel for */
     HIPGPT_ERR_LAUNCH = -3,       /* the HIP launch itself failed             */
-    HIPGPT_ERR_WORKSPACE = -4     /* workspace missing or too small           */
+    HIPGPT_ERR_WORKSPACE = -4,    /* workspace missing or too small           */
+    HIPGPT_ERR_SCRATCH = -5       /* beyond the no-allocation entry's scratch */
 };
 
 enum { HIPGPT_F32 = 0, HIPGPT_BF16 = 1 };
@@ -64,6 +65,19 @@ int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv,
                                int S, int E, int H, int causal,
                                void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
+
+/* No counterpart in HipGPT.  hipgpt_attn_bwd_qkv_planar without a workspace
+ * argument, for callers that cannot allocate: code under HIP graph capture,
+ * tight serving/training loops, harnesses that forbid hipMalloc.  It calls no
+ * allocator; its B*H*S row-dot workspace is a fixed 4 MiB array per GPU
+ * inside the library, so B*H*S must be at most 1048576 (else
+ * HIPGPT_ERR_SCRATCH, nothing launched).  Calls that overlap on one GPU (two
+ * streams, or host threads) share that array and race; serialise them.
+ * Results are identical to hipgpt_attn_bwd_qkv_planar's. */
+int hipgpt_attn_bwd_qkv_planar_noalloc(const float* grad_out, const float* qkv,
+                                       const float* probs, float* grad_qkv,
+                                       int B, int S, int E, int H, int causal,
+                                       hipStream_t stream);
 
 /* Training pair without the [B][H][S][S] probs buffer (FlashAttention-2's
  * forward/backward split).  No counterpart in HipGPT, whose backward reads the
