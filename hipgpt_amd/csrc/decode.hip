@@ -186,28 +186,63 @@ __global__ __launch_bounds__(DEC_NW * 64) void decode_partial_kernel(AttnArgs a,
     }
 }
 
+// Merge of the splits of one (b, h) row, with the splits in parallel: the
+// (m, l) pairs are reduced by all 256 threads (block max, then block sum of
+// l_s 2^(m_s - M)); the O rows by DP/4 lanes per split row (one float4 each)
+// and 1024/DP split rows at a time, combined through LDS.
+constexpr int RED_T = 256;
+
 template <int DP>
-__global__ __launch_bounds__(64) void decode_reduce_kernel(AttnArgs a, int nsplit, const float* ws, int* advance_lens,
-                                                           int max_len) {
+__global__ __launch_bounds__(RED_T) void decode_reduce_kernel(AttnArgs a, int nsplit, const float* ws,
+                                                              int* advance_lens, int max_len) {
+    constexpr int LP = DP / 4;         // lanes per split row
+    constexpr int SG = RED_T / LP;     // split rows in flight
+    __shared__ float red[RED_T / 64];
+    __shared__ __attribute__((aligned(16))) float s_o[SG][DP];
     const int bh = blockIdx.x;
     const int BH = a.B * a.H;
     const int b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // KV-cache step: the head-0 workgroup advances its sequence (no reduce
     // workgroup reads lens, and the partial kernel has completed)
-    if (advance_lens && h == 0 && threadIdx.x == 0) {
+    if (advance_lens && h == 0 && tid == 0) {
         const int n = advance_lens[b];
         if (n >= 0 && n < max_len) advance_lens[b] = n + 1;
     }
     const float* wml = ws + (int64_t)bh * nsplit * 2;
     const float* wo = ws + (int64_t)BH * nsplit * 2 + (int64_t)bh * nsplit * DP;
-    float M = kMaxInit;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, wml[2 * s]);
+
+    float mx = kMaxInit;
+    for (int s = tid; s < nsplit; s += RED_T) mx = fmaxf(mx, wml[2 * s]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < RED_T / 64; ++w) M = fmaxf(M, red[w]);
+    __syncthreads();
+    float ls = 0.f;
+    for (int s = tid; s < nsplit; s += RED_T) ls = fmaf(wml[2 * s + 1], fast_exp2(wml[2 * s] - M), ls);
+    ls = wave_sum(ls);
+    if (lane == 0) red[wave] = ls;
+    __syncthreads();
     float L = 0.f;
-    for (int s = 0; s < nsplit; ++s) L = fmaf(wml[2 * s + 1], fast_exp2(wml[2 * s] - M), L);
+#pragma unroll
+    for (int w = 0; w < RED_T / 64; ++w) L += red[w];
+
+    const int sub = tid % LP, sg = tid / LP;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s = sg; s < nsplit; s += SG) {
+        const float w = fast_exp2(wml[2 * s] - M);
+        acc += w * *reinterpret_cast<const floatx4*>(wo + (int64_t)s * DP + sub * 4);
+    }
+    *reinterpret_cast<floatx4*>(&s_o[sg][sub * 4]) = acc;
+    __syncthreads();
     const float linv = 1.0f / fmaxf(L, 1e-20f);
-    for (int d = threadIdx.x; d < a.D; d += 64) {
+    for (int d = tid; d < a.D; d += RED_T) {
         float O = 0.f;
-        for (int s = 0; s < nsplit; ++s) O = fmaf(wo[(int64_t)s * DP + d], fast_exp2(wml[2 * s] - M), O);
+#pragma unroll
+        for (int g = 0; g < SG; ++g) O += s_o[g][d];
         a.o[b * a.o_bs + h * a.o_hs + d] = O * linv;
     }
 }
@@ -243,7 +278,7 @@ hipError_t launch_decode_dp(const AttnArgs& a, const KvcArgs* kc, int nsplit, fl
     int* adv = kc && kc->advance ? kc->lens : nullptr;
     const int max_len = kc ? kc->max_len : 0;
     if (nsplit > 1) {
-        hipLaunchKernelGGL((decode_reduce_kernel<DP>), dim3((unsigned)BH), dim3(64), 0, stream, a, nsplit,
+        hipLaunchKernelGGL((decode_reduce_kernel<DP>), dim3((unsigned)BH), dim3(RED_T), 0, stream, a, nsplit,
                            static_cast<const float*>(ws), adv, max_len);
         e = hipGetLastError();
     } else if (adv) {

@@ -44,6 +44,15 @@ def test_library_exports_every_declared_symbol():
         assert f" T {sym}" in out.stdout, sym
 
 
+def test_no_undefined_library_symbols():
+    """Every symbol of the library's own namespace is defined (a kernel whose
+    host launch stub the compiler dropped shows up here as undefined, and the
+    library would fail to load on the GPU box)."""
+    out = subprocess.run(["nm", "-u", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    missing = [ln.split()[-1] for ln in out.splitlines() if "6hipgpt" in ln]
+    assert not missing, missing
+
+
 def test_strerror_and_host_validation():
     L = _lib.lib()
     assert L.hipgpt_attn_strerror(0) == b"ok"

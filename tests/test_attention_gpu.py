@@ -202,6 +202,21 @@ def test_bf16_matches_f64_on_rounded_inputs(dev, B, Sq, Sk, H, D, causal, with_p
     assert np.abs(got - full).max() <= 0.1
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,Sq,Sk,H,D", [(1, 300, 300, 2, 64), (2, 129, 129, 3, 32), (1, 50, 200, 2, 64),
+                                         (1, 257, 1000, 1, 64), (3, 128, 128, 2, 32), (1, 33, 33, 1, 64),
+                                         (1, 1, 1, 1, 64), (2, 500, 520, 2, 32)])
+def test_bf16_more_shapes(dev, B, Sq, Sk, H, D, causal):
+    """bf16 without probs at D = 32 / 64: several 128-query blocks, ragged
+    Sq / Sk, Sq != Sk (causal bottom-right offset), a single row; against
+    float64 on the bf16-rounded inputs."""
+    (q, k, v), (tq, tk, tv), (rq, rk, rv) = _bf16_inputs(Sq * 11 + Sk + D, B, Sq, Sk, H, D)
+    want, _ = O.attention(rq, rk, rv, causal=causal, f64=True)
+    got = host(A.attention(tq, tk, tv, causal=causal))
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= TOL_BF16
+
+
 # ---------------------------------------------------------------- unfused helpers
 # Row kernels (D = 32/64/128, aligned): S on and off the 32-row tile grid, the
 # register-resident softmax at 256/512/1024/2048 columns and the sweep softmax
