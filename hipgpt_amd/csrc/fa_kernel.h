@@ -52,6 +52,11 @@ __device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is.
 // SRT > 0 (probs only): when a wave's key tiles span at most SRT stages, the
 // max/sum sweep keeps every score tile in registers and the probs sweep reads
 // them back instead of recomputing Q K^T (it stages V only).
+// SRT < 0 (probs only, rows longer than that): the max/sum sweep stores each
+// masked score tile into the probs buffer, where the probs sweep reads it back
+// and overwrites it with P -- two products instead of three (no second Q K^T,
+// no K staging) for one more write and read of the probs rows.  Each lane
+// reads back only what it wrote, in the same sweep order.
 template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 struct FaKernel {
     static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");
@@ -59,6 +64,7 @@ struct FaKernel {
     static constexpr int NW = NQS * NKS;
     static constexpr int NT = NW * 64;
     static constexpr int NDB = DP / 32;
+    static constexpr bool SPILL = SRT < 0;
     using E = typename TR::elem;
 
     // LDS: two stage buffers of NKS (K tile + V^T tile); the end-of-kernel
@@ -241,16 +247,45 @@ struct FaKernel {
 
         Stager st;
         st.init(Kp, Vp, a.k_ts, a.v_ts, Sk, a.D, tid);
+        // Spilled scores of tile t (register r <-> key tb + acc_key(r, hf)):
+        // keys past Sk and rows past Sq were never written and read as -inf.
+        auto spilled_scores = [&](const float* prow, int t) -> floatx16 {
+            floatx16 s;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int k0 = t * BK + 8 * g + 4 * hf;
+                floatx4 v = {kNegInf, kNegInf, kNegInf, kNegInf};
+                if (qi < Sq) {
+                    if (k0 + 3 < Sk) {
+                        v = *reinterpret_cast<const floatx4*>(prow + k0);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (k0 + j < Sk) v[j] = prow[k0 + j];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[4 * g + j] = v[j];
+            }
+            return s;
+        };
         // ------------------------------------------------------------------
         // One stage of compute on LDS buffer (i & 1).  MODE 0: online softmax
-        // + PV.  MODE 1: max/sum only.  MODE 2: probs store + PV with the
-        // final (m, l).
+        // + PV.  MODE 1: max/sum only (SPILL: and the scores stored).  MODE 2:
+        // probs store + PV with the final (m, l) (SPILL: from the stored scores).
+        floatx16 s_next;  // SPILL, probs sweep: the next tile's stored scores, loaded one tile ahead
         auto compute = [&](auto mode_tag, int i, float mlog, float* prow, bool pvec) {
             constexpr int MODE = decltype(mode_tag)::value;
             const E* cur = lds + (i & 1) * STAGE_ELEMS;
             const int t = i * NKS + ks;
             if (t >= wtiles) return;
-            floatx16 s = tile_scores(cur, t);
+            floatx16 s;
+            if constexpr (SPILL && MODE == 2) {
+                s = s_next;
+                if (t + NKS < wtiles) s_next = spilled_scores(prow, t + NKS);
+            } else {
+                s = tile_scores(cur, t);
+            }
             typename TR::VReg vreg;
             if (MODE != 1) TR::load_v(vreg, vt_of(cur, t), c, hf);  // in flight during the softmax
             if (MODE == 0) {
@@ -276,6 +311,7 @@ struct FaKernel {
                 l_run += ls;  // this lane half's partial; the halves are summed after the sweep
                 TR::pv(vreg, s, o, c, hf);
             } else if (MODE == 1) {
+                if (SPILL && qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 const float m_new = vmax(m_run, tile_max(s) * sc);
                 float ls = 0.f;
 #pragma unroll
@@ -297,18 +333,19 @@ struct FaKernel {
         // has two stages of compute to land.
         auto sweep = [&](auto mode_tag, float mlog, float* prow, bool pvec) {
             constexpr bool WV = decltype(mode_tag)::value != 1;  // the max/sum sweep stages no V
+            constexpr bool WK = !(SPILL && decltype(mode_tag)::value == 2);  // nor the spilled probs sweep K
             if (nstages > 0) {
-                st.template load<0, WV>(0, tid);
-                if (PF == 2 && nstages > 1) st.template load<PF - 1, WV>(1, tid);
-                st.template store<0, WV>(lds, tid);
+                st.template load<0, WV, WK>(0, tid);
+                if (PF == 2 && nstages > 1) st.template load<PF - 1, WV, WK>(1, tid);
+                st.template store<0, WV, WK>(lds, tid);
             }
             __syncthreads();
             auto iter = [&](int i, auto slot_tag) {
                 constexpr int SL = decltype(slot_tag)::value;  // slot free for new loads
                 constexpr int NX = PF == 2 ? 1 - SL : 0;      // slot holding stage i+1
-                if (i + PF < nstages) st.template load<SL, WV>(i + PF, tid);
+                if (i + PF < nstages) st.template load<SL, WV, WK>(i + PF, tid);
                 compute(mode_tag, i, mlog, prow, pvec);
-                if (i + 1 < nstages) st.template store<NX, WV>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                if (i + 1 < nstages) st.template store<NX, WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
                 __syncthreads();
             };
             for (int i = 0; i < nstages; i += PF) {
@@ -413,10 +450,12 @@ struct FaKernel {
                 zero_probs_tail(a.probs + (int64_t)bh * Sq * Sk, qw0, Sq, Sk, tr.wtiles * BK, lane, pv0);
             }
 #endif
+            float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
+            const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
             if constexpr (SRT > 0)
                 sweep_res(std::false_type{}, 0.f, nullptr, false);
             else
-                sweep(std::integral_constant<int, 1>{}, 0.f, nullptr, false);
+                sweep(std::integral_constant<int, 1>{}, 0.f, probs_bh + (int64_t)qi * Sk, pvec);
             if (NKS > 1) {
                 m_slot[role * 64 + lane] = m_run;
                 l_slot[role * 64 + lane] = l_run;
@@ -435,8 +474,9 @@ struct FaKernel {
             // P = exp2(s' - m) / l = exp2(s' - (m + log2 l)): the normalisation
             // rides in the exponent (no multiply per score)
             const float mlog = m_run + __builtin_amdgcn_logf(fmaxf(l_run, 1e-20f));
-            float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
-            const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
+            if constexpr (SPILL) {
+                if (ks < wtiles) s_next = spilled_scores(probs_bh + (int64_t)qi * Sk, ks);
+            }
             if constexpr (SRT > 0)
                 sweep_res(std::true_type{}, mlog, probs_bh + (int64_t)qi * Sk, pvec);
             else
@@ -528,6 +568,18 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// Probs rows that do not fit the score-resident stages spill their scores to
+// the probs buffer between the sweeps (1) or recompute Q K^T (0).  Reading a
+// spilled 32x32 tile back costs 4 KB per query sub-block whatever the head
+// size; recomputing it costs a staged K tile (32 * D * 4 bytes, shared by the
+// workgroup) and 32 * 32 * D MFMA work.  The spill measured faster on fp32
+// operands at D = 128 (B4 H16 S2048: 1623 -> 1504 us for the drop-in
+// launcher) and slower at D = 64 (B8 H12 S1024: 327 -> 388 us), so it is
+// used for fp32 operands with a padded head size of 128 or more.
+#ifndef HIPGPT_SCORE_SPILL
+#define HIPGPT_SCORE_SPILL 1
+#endif
+
 // Score-resident stages of a traits type (PROBS_RES_STAGES; 0 = the probs
 // sweeps recompute Q K^T).
 template <class TR, class = void>
@@ -540,11 +592,19 @@ struct probs_res_stages<TR, std::void_t<decltype(TR::PROBS_RES_STAGES)>> {
 template <class TR, int NQS, int NKS, int PF, bool VEC>
 hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
     constexpr int SRT = probs_res_stages<TR>::value;
+    constexpr bool kSpill = HIPGPT_SCORE_SPILL && VEC && sizeof(typename TR::elem) == 4 && TR::DP >= 128;
     if constexpr (SRT > 0) {
         // every wave's key tiles fit the resident stages (Sk <= SRT * NKS * 32)
         if (probs && ((a.Sk + BK - 1) / BK + NKS - 1) / NKS <= SRT)
             return causal ? launch_fa<TR, NQS, NKS, PF, true, true, VEC, SRT>(a, s)
                           : launch_fa<TR, NQS, NKS, PF, false, true, VEC, SRT>(a, s);
+    }
+    // longer rows: the scores are spilled to the probs buffer between the
+    // sweeps (16-byte aligned probs rows)
+    if constexpr (kSpill) {
+        if (probs && (a.Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0)
+            return causal ? launch_fa<TR, NQS, NKS, PF, true, true, VEC, -1>(a, s)
+                          : launch_fa<TR, NQS, NKS, PF, false, true, VEC, -1>(a, s);
     }
     if (causal)
         return probs ? launch_fa<TR, NQS, NKS, PF, true, true, VEC>(a, s)
