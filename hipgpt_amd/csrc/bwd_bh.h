@@ -105,6 +105,28 @@ __device__ __forceinline__ void set_flag(int* flag, int v) {
 // LDS banks).
 __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 * h + (s & 7); }
 
+// Stored P of query tile i and key kj in the accumulator's order (register r
+// <-> query i*32 + acc_key(r, h), lane <-> key kj) from the (b, h) slice
+// `pr` of the [S][S] probs; keys past S read as zero through an
+// out-of-range offset.  The buffer range check covers the vector offset (and
+// the immediate) only, never the scalar offset: a whole tile in range puts
+// each register's row offset in the scalar operand, the last tile of a ragged
+// S (rows past S) folds it into the vector offset so those rows read as zero.
+__device__ __forceinline__ void load_p_tile(floatx16& pv, __amdgpu_buffer_rsrc_t pr, int i, int kj, bool kval, int hf,
+                                            int S) {
+    const int S4 = S * 4;
+    const int vo = kval ? (i * BK + 4 * hf) * S4 + kj * 4 : 0x40000000;
+    if (i * BK + BK <= S) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            pv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, vo, (8 * (r >> 2) + (r & 3)) * S4, 0));
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            pv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, vo + (8 * (r >> 2) + (r & 3)) * S4, 0, 0));
+    }
+}
+
 template <bool CAUSAL, bool PROBS>
 __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
@@ -334,27 +356,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         }
     }
 
-    // Stored probs, phase 2: P of query tile i in the accumulator's order
-    // (register r <-> query i*32 + acc_key(r, h), lane <-> key kj); keys
-    // past S read as zero through an out-of-range offset.  The buffer range
-    // check covers the vector offset (and the immediate) only, never the
-    // scalar offset: a whole tile in range puts each register's row offset in
-    // the scalar operand, the last tile of a ragged S (rows past S) folds it
-    // into the vector offset so those rows read as zero.
-    auto load_pk = [&](floatx16& pv, int i) {
-        const int vo = kval ? (i * BK + 4 * hf) * S4 + kj * 4 : 0x40000000;
-        if (i * BK + BK <= S) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                pv[r] = __builtin_bit_cast(float,
-                                           __builtin_amdgcn_raw_buffer_load_b32(pr, vo, (8 * (r >> 2) + (r & 3)) * S4, 0));
-        } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                pv[r] = __builtin_bit_cast(float,
-                                           __builtin_amdgcn_raw_buffer_load_b32(pr, vo + (8 * (r >> 2) + (r & 3)) * S4, 0, 0));
-        }
-    };
+    // Stored probs, phase 2: P of query tile i in the accumulator's order.
+    auto load_pk = [&](floatx16& pv, int i) { load_p_tile(pv, pr, i, kj, kval, hf, S); };
     floatx16 pnext;
     if constexpr (PROBS) load_pk(pnext, kt);
 
@@ -500,6 +503,308 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Stored probs without a causal mask (the reference's drop-in call): every P
+// tile is read from memory once.
+//
+// At step t every wave works on query tile t against its own key tile j, so
+// the row sums Dq_t = sum_j rowsum(P_tj o dP_tj) complete with one
+// workgroup barrier per step.  A wave forms dP_tj = dO_t V_j^T a step ahead,
+// sums P o dP over its 32 keys (transposed through its LDS scratch) and
+// publishes the 32 partial sums; after the barrier each wave adds the
+// partials in key-tile order.  dS = P o (dP - Dq), dV^T += dO^T P and
+// dK^T += Q^T dS then use the P tile still in registers.  dQ of query tile t
+// is the sum of the waves' 32x32 terms dS_tj K_j: each wave leaves its term
+// in a double-buffered LDS area and, after the next barrier, every wave adds
+// the terms of four of the 32 rows in key-tile order and writes them.  Q and
+// dO tiles stream through a three-slot LDS ring, staged by all threads two
+// steps ahead.  Per step a wave runs 64 MFMAs (dP, dV, dK, dQ) -- the
+// two-phase kernel above runs 80 and reads P twice -- and waits on no flag.
+// All summation orders are fixed: results are deterministic.
+namespace nc {
+// LDS layout in floats.  The per-wave scratch and the ring come first: DS
+// instructions take immediate offsets below 64 KB only, and those two areas
+// take most of the accesses.
+constexpr int TILE = BK * RP;  // one Q or dO tile, row-major with pitch RP
+constexpr int SLOTS = 3;       // ring slots, each a Q tile then a dO tile
+constexpr int XS = 0;          // per-wave scratch [NW][BK][XP]
+constexpr int RING = XS + NW * BK * XP;
+constexpr int PD = RING + SLOTS * 2 * TILE;  // partial row sums [2][NW][BK]
+constexpr int DQP = PD + 2 * NW * BK;        // dQ terms [2][NW][BK][PP]
+constexpr int TOTAL = DQP + 2 * NW * BK * PP;
+constexpr int kLdsBytes = TOTAL * 4;
+// The step's Dq sits in the scratch rows' pitch padding: query q at row q / 4,
+// column BK + q % 4.
+constexpr int DQCOL = BK;
+static_assert(XP >= BK + 4, "room for the step's Dq in the scratch pitch");
+static_assert(PD * 4 <= 65536, "scratch and ring within the DS immediate range");
+static_assert(kLdsBytes <= 160 * 1024, "LDS of the single-read kernel");
+static_assert(NW * 32 == BK * CPR, "one 16-byte chunk of a Q or dO tile per thread of half the workgroup");
+}  // namespace nc
+
+// Workgroup barrier that publishes LDS writes only: each wave waits for its
+// own LDS accesses, not for its global loads in flight (a workgroup-scope
+// fence, as in __syncthreads, would also wait for the prefetched P tiles and
+// ring rows).  The memory clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// A per-lane LDS float offset the compiler cannot fold into constants: the
+// accesses through it then carry their constant part as an immediate offset
+// (below 64 KB) instead of a full address computed per access.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 31, hf = lane >> 5;
+    const int bhi = blockIdx.x;
+    const int b = bhi / a.H, h = bhi % a.H;
+    const int S = a.S, nt = (S + BK - 1) / BK;
+    const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
+    const bool active = wave < nt;  // the wave owns key tile `wave`
+    const int kj = wave * BK + c;
+    const bool kval = kj < S;
+    float* const X = lds + nc::XS + wave * BK * XP;
+
+    // Q / dO ring: tile i sits in slot i % 3 (Q, then dO).  Waves 0-3 stage
+    // the Q tile, waves 4-7 the dO tile, one 16-byte chunk per thread; rows
+    // past S read as zero.  Tiles past the last (i < nt + 3) are staged too:
+    // they read as zero, and their slot's tile i-3 has been read by then.
+    RowLoader rl;
+    rl.init((wave < NW / 2 ? a.q : a.go) + base, a.ts, S, D);
+    const int sf = tid & (NW * 32 - 1);
+    const int srow = sf / CPR, scc = sf % CPR;
+    const int soff = (wave < NW / 2 ? 0 : nc::TILE) + srow * RP + 4 * scc;
+    auto slot = [&](int i) { return lds + nc::RING + (i % nc::SLOTS) * 2 * nc::TILE; };
+    auto ring_load = [&](int i) { return rl.load(i * BK + srow, scc); };
+    auto ring_store = [&](int i, const floatx4& v) { *reinterpret_cast<floatx4*>(slot(i) + soff) = v; };
+
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.probs) + (int64_t)bhi * S * S, 0, S * S * 4, kBufferFlags);
+
+    // The wave's keys: V (B operand of dP, lane (c, h) holding dims
+    // 16h .. 16h+15 of key kj) and K as the B operand of the dQ product over
+    // keys (step s: key dq_key(s, h), dim c), read back through the scratch.
+    // Every workgroup starts at once, so the first loads arrive as one burst
+    // over the whole device: only what the first step needs is requested
+    // before it (ring tiles 0 and 1, V, P of tile 0, K, in order of first
+    // use); P of tile 1 and ring tile 2 follow once the first step runs.
+    float vr[D / 2], kq[16];
+    floatx16 p, pn;  // P of the step's query tile and of the next one
+    floatx4 r0 = ring_load(0), r1 = ring_load(1);
+    floatx4 kv[D / 8], vv[D / 8];
+    RowLoader kl, vl;
+    kl.init(a.k + base, a.ts, S, D);
+    vl.init(a.v + base, a.ts, S, D);
+    if (active) {
+#pragma unroll
+        for (int s = 0; s < D / 8; ++s) vv[s] = vl.load(kj, hf * (D / 8) + s);
+        load_p_tile(p, pr, 0, kj, kval, hf, S);
+#pragma unroll
+        for (int s = 0; s < D / 8; ++s) kv[s] = kl.load(kj, hf * (D / 8) + s);
+    }
+    ring_store(0, r0);
+    ring_store(1, r1);
+    if (!active) {
+        // a wave past the last key tile zeroes its partial-sum and dQ-term
+        // slots once, so the sums over all NW waves need no selects
+        lds[nc::PD + (hf * NW + wave) * BK + c] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2 * BK * (BK / 4) / 64; ++k) {
+            const int f = lane + 64 * k;  // [parity][row][chunk of four dims]
+            const int par = f / (BK * BK / 4), row = (f / (BK / 4)) % BK, c4 = f % (BK / 4);
+            *reinterpret_cast<floatx4*>(lds + nc::DQP + ((par * NW + wave) * BK + row) * PP + 4 * c4) =
+                floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // Per-lane bases of the areas above 64 KB (constant parts as immediates).
+    const float* const pdl = lds + opaque(nc::PD + c);                            // + (parity * NW + v) * BK
+    float* const dqw = lds + opaque(nc::DQP + wave * BK * PP + 4 * hf * PP + c);  // + parity * NW*BK*PP + row * PP
+    const int rrow = 4 * wave + (lane >> 4), rd2 = 2 * (lane & 15);
+    const float* const dqr0 = lds + opaque(nc::DQP + rrow * PP + rd2);            // + v * BK*PP
+    const float* const dqr1 = lds + opaque(nc::DQP + NW * BK * PP + rrow * PP + rd2);
+
+    // dP = dO_i V_j^T of the dO tile `gt` (register r <-> query acc_key(r, h),
+    // lane <-> key), the chain starting from zero.
+    auto dp_tile = [&](const float* gt) {
+        const float* rr = gt + c * RP + hf * (D / 2);
+        floatx4 dv[D / 8];
+#pragma unroll
+        for (int j = 0; j < D / 8; ++j) dv[j] = *reinterpret_cast<const floatx4*>(rr + 4 * j);
+        floatx16 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(dv[0][0], vr[0], floatx16{}, 0, 0, 0);
+#pragma unroll
+        for (int k = 1; k < D / 2; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(dv[k >> 2][k & 3], vr[k], acc, 0, 0, 0);
+        return acc;
+    };
+    // Row sums of P o dP of a query tile over this wave's keys into the PD
+    // entry of parity PAR: the product is stored transposed ([key][query])
+    // and lane (c, h) adds keys 16h .. 16h+15 of query c, the two halves
+    // starting eight keys apart (disjoint banks); then the halves are added.
+    auto partial = [&](auto par_tag, const floatx16& pv, const floatx16& dpv) {
+        constexpr int PAR = decltype(par_tag)::value;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
+                floatx4{pv[4 * g] * dpv[4 * g], pv[4 * g + 1] * dpv[4 * g + 1], pv[4 * g + 2] * dpv[4 * g + 2],
+                        pv[4 * g + 3] * dpv[4 * g + 3]};
+        const float* xa = X + (24 * hf) * XP + c;  // keys 24h + u, u < 8 (h = 1: 24 .. 31)
+        const float* xb = X + (8 * hf) * XP + c;   // keys 8h + u, u >= 8 (h = 1: 16 .. 23)
+        float s = 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += xa[u * XP];
+#pragma unroll
+        for (int u = 8; u < 16; ++u) s += xb[u * XP];
+        s += __shfl_xor(s, 32);
+        if (hf == 0) lds[nc::PD + (PAR * NW + wave) * BK + c] = s;
+    };
+
+    lds_barrier();  // ring tiles 0 and 1
+
+    floatx16 dp, dpn;  // dP of the step's query tile and of the next one
+    if (active) {
+#pragma unroll
+        for (int s = 0; s < D / 8; ++s)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) vr[4 * s + j] = vv[s][j];
+        dp = dp_tile(slot(0) + nc::TILE);
+        partial(std::integral_constant<int, 0>{}, p, dp);
+    }
+
+    // dQ rows of query tile i (parity PAR): wave w adds rows 4w .. 4w+3 of the
+    // waves' terms (two dims per lane) in key-tile order and writes them
+    // through a buffer resource ending at row S-1 (rows past S are dropped).
+    const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(
+        a.dq + base, 0, (int)(((int64_t)(S - 1) * a.ts + D) * 4), kBufferFlags);
+    const int row4 = a.ts * 4;
+    auto reduce_dq = [&](auto par_tag, int i) {
+        constexpr int PAR = decltype(par_tag)::value;
+        const float* src = PAR ? dqr1 : dqr0;
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {  // terms past the last key tile are zeros
+            const float2 x = *reinterpret_cast<const float2*>(src + v * BK * PP);
+            s0 += x.x;
+            s1 += x.y;
+        }
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a.scale * s0), __float_as_uint(a.scale * s1)}, dqr,
+                                              (i * BK + rrow) * row4 + rd2 * 4, 0, 0);
+    };
+
+    floatx16 accv, acck;  // dV^T, dK^T (unscaled): register r <-> dim acc_key(r, h), lane <-> key
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accv[r] = acck[r] = 0.f;
+    lds_barrier();  // step 0's partial row sums
+    floatx4 rn = ring_load(2);
+    if (active) {
+        if (nt > 1) load_p_tile(pn, pr, 1, kj, kval, hf, S);
+        // K through the scratch (the partial sums' reads of it are done)
+#pragma unroll
+        for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = kv[s];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) kq[s] = X[dq_key(s, hf) * XP + c];
+    }
+
+    // One step of an active wave on query tile t (t % 2 == PAR): pc / dc hold
+    // P / dP of tile t, pnx P of tile t+1; a step with a successor (LAST
+    // false) forms dnx = dP of tile t+1 and its partial row sums, and loads P
+    // of tile t+2 into pc (the last tile again past the end).  Steps
+    // alternate the buffers' roles, so no registers are copied.
+    auto step = [&](auto last_tag, auto par_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dc, floatx16& dnx) {
+        constexpr bool LAST = decltype(last_tag)::value;
+        constexpr int PAR = decltype(par_tag)::value;
+        const float* qt = slot(t);
+        const float* gt = qt + nc::TILE;
+        // Dq of query tile t (lane: query c): the partials in key-tile order
+        // (zeros past the last key tile), kept in the scratch's padding for
+        // the register-order reads below
+        float dsum = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) dsum += pdl[(PAR * NW + v) * BK];
+        if (hf == 0) X[(c >> 2) * XP + nc::DQCOL + (c & 3)] = dsum;
+        // dV^T += dO^T P: A[d][query] read from the row-major dO tile
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            accv = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[acc_key(r, hf) * RP + c], pc[r], accv, 0, 0, 0);
+        floatx16 ds;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const floatx4 d4 = *reinterpret_cast<const floatx4*>(X + (2 * g + hf) * XP + nc::DQCOL);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ds[4 * g + j] = pc[4 * g + j] * (dc[4 * g + j] - d4[j]);
+        }
+        // dK^T += Q^T dS
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            acck = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[acc_key(r, hf) * RP + c], ds[r], acck, 0, 0, 0);
+        // dQ term dS K: dS^T through the scratch ([key][query]), A[query][key] = X[key][query]
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
+                floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
+        floatx16 aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(0, hf) * XP + c], kq[0], floatx16{}, 0, 0, 0);
+#pragma unroll
+        for (int s = 1; s < 16; ++s)
+            aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
+        if constexpr (!LAST) {
+            // the next query tile: dP, the partial row sums, and P two tiles ahead
+            dnx = dp_tile(slot(t + 1) + nc::TILE);
+            load_p_tile(pc, pr, t + 2 < nt ? t + 2 : nt - 1, kj, kval, hf, S);
+            partial(std::integral_constant<int, 1 - PAR>{}, pnx, dnx);
+        }
+        // this wave's dQ term of query tile t (register r <-> query acc_key(r, h), lane <-> dim c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dqw[PAR * NW * BK * PP + (8 * (r >> 2) + (r & 3)) * PP] = aq[r];
+    };
+    // Every wave after its step on tile t: the dQ rows of tile t-1, the ring,
+    // the barrier.
+    auto finish = [&](auto par_tag, int t) {
+        constexpr int PAR = decltype(par_tag)::value;
+        if (t > 0) reduce_dq(std::integral_constant<int, 1 - PAR>{}, t - 1);
+        ring_store(t + 2, rn);  // its slot held tile t-1, last read before the previous barrier
+        rn = ring_load(t + 3);
+        lds_barrier();
+    };
+    using Even = std::integral_constant<int, 0>;
+    using Odd = std::integral_constant<int, 1>;
+    int t = 0;
+    for (; t + 2 < nt; t += 2) {
+        if (active) step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
+        finish(Even{}, t);
+        if (active) step(std::false_type{}, Odd{}, t + 1, pn, p, dpn, dp);
+        finish(Odd{}, t + 1);
+    }
+    if (t + 1 < nt) {
+        if (active) step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
+        finish(Even{}, t);
+        if (active) step(std::true_type{}, Odd{}, t + 1, pn, p, dpn, dp);
+        finish(Odd{}, t + 1);
+        reduce_dq(Odd{}, t + 1);
+    } else {
+        if (active) step(std::true_type{}, Even{}, t, p, pn, dp, dpn);
+        finish(Even{}, t);
+        reduce_dq(Even{}, t);
+    }
+
+    if (active && kval) {
+        float* dvp = a.dv + base + (int64_t)kj * a.ts;
+        float* dkp = a.dk + base + (int64_t)kj * a.ts;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 8 * g + 4 * hf;
+            *reinterpret_cast<floatx4*>(dvp + d0) = floatx4{accv[4 * g], accv[4 * g + 1], accv[4 * g + 2], accv[4 * g + 3]};
+            *reinterpret_cast<floatx4*>(dkp + d0) = floatx4{a.scale * acck[4 * g], a.scale * acck[4 * g + 1],
+                                                            a.scale * acck[4 * g + 2], a.scale * acck[4 * g + 3]};
+        }
+    }
+}
+
 }  // namespace bh
 
 // D = 32, S <= 256 and the tiled kernels' layout conditions (bwd_tiled_ok);
@@ -510,23 +815,28 @@ inline bool bh_ok(const BwdArgs& a) {
     return !a.probs || (a.S % 4 == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15u) == 0);
 }
 
-template <bool CAUSAL, bool PROBS>
-hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
-    const int64_t grid = (int64_t)a.B * a.H;
-    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    auto kern = bh::bwd_bh_kernel<CAUSAL, PROBS>;
-    // The dynamic-LDS limit is raised once per device (bit d of attr_set).
-    static std::atomic<unsigned long long> attr_set{0};
+// Raise a kernel's dynamic-LDS limit once per device (bit d of attr_set).
+inline hipError_t raise_lds_limit(const void* kern, int bytes, std::atomic<unsigned long long>& attr_set) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const unsigned long long bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
     if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                bh::kMaxLdsBytes);
+        e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_release);
     }
+    return hipSuccess;
+}
+
+template <bool CAUSAL, bool PROBS>
+hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
+    const int64_t grid = (int64_t)a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    auto kern = bh::bwd_bh_kernel<CAUSAL, PROBS>;
+    static std::atomic<unsigned long long> attr_set{0};
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(kern), bh::kMaxLdsBytes, attr_set);
+    if (e != hipSuccess) return e;
     const int Sp = (a.S + BK - 1) / BK * BK;
     const size_t lds = (size_t)bh::layout(Sp).total * 4;
     BwdArgs args = a;
@@ -537,7 +847,24 @@ hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Stored probs without a causal mask: the single-read kernel (1) or the
+// two-phase kernel (0).
+#ifndef HIPGPT_BH_SINGLE_READ
+#define HIPGPT_BH_SINGLE_READ 1
+#endif
+
+inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
+    const int64_t grid = (int64_t)a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    static std::atomic<unsigned long long> attr_set{0};
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(bh::bwd_bh_probs_kernel), bh::nc::kLdsBytes, attr_set);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(bh::bwd_bh_probs_kernel, dim3((unsigned)grid), dim3(bh::NW * 64), bh::nc::kLdsBytes, s, a);
+    return hipGetLastError();
+}
+
 inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
+    if (a.probs && !a.causal && HIPGPT_BH_SINGLE_READ) return launch_bh_probs(a, s);
     if (a.probs) return a.causal ? launch_bh_mode<true, true>(a, s) : launch_bh_mode<false, true>(a, s);
     return a.causal ? launch_bh_mode<true, false>(a, s) : launch_bh_mode<false, false>(a, s);
 }
