@@ -84,6 +84,7 @@ CONFIGS = {
     "c1_bwd": (32, 8, 256, 256, 32, True, "f32", True, "bwd"),
     "c1_bwd_legacy": (32, 8, 256, 256, 32, False, "f32", True, "bwd"),
     "c2_bwd": (32, 8, 256, 256, 64, True, "f32", True, "bwd"),
+    "c2_bwd_legacy": (32, 8, 256, 256, 64, False, "f32", True, "bwd"),
     # The probs-free training pair at the same shapes: forward writing O and the
     # row log-sum-exp, and the backward that recomputes P from it.
     "c1_fwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "fwd_lse"),

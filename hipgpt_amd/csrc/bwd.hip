@@ -22,6 +22,7 @@
 // Causal (extended API only) skips tiles of P that lie wholly above the
 // diagonal, where a causal forward wrote zeros.
 #include "bwd_bh.h"
+#include "bwd_bh64.h"
 #include "bwd_tiled.h"
 #include "common.h"
 #include "fa_common.h"
@@ -330,13 +331,16 @@ bool bwd_tiled_ok(const BwdArgs& a) {
            ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
 }
 
-bool bwd_uses_workspace(const BwdArgs& a) { return a.probs && !(bwd_tiled_ok(a) && bwd::bh_ok(a)); }
+bool bwd_uses_workspace(const BwdArgs& a) {
+    return a.probs && !(bwd_tiled_ok(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
+}
 
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     // recompute mode (no probs): tiled kernels only
     if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
         if (bwd::bh_ok(a)) return bwd::launch_bh(a, s);
+        if (bwd::bh_probs64_ok(a)) return bwd::launch_bh_probs64(a, s);
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
         return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);

@@ -37,7 +37,8 @@
 // with the loaded P) waits per tile for that flag.  Causally the light wave
 // of each SIMD pair owns both of the pair's query tiles, the heavy partner's
 // first, so the wave with the most phase-2 jobs starts them at once.  P is
-// read twice (once per phase).
+// read twice (once per phase).  Without the causal mask (the reference's
+// drop-in call) bwd_bh_probs_kernel below runs instead and reads P once.
 //
 // One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal

@@ -149,12 +149,14 @@ CONFIGS = {  # the BASELINE forward configs whose probs buffer fits the oracle's
 }
 
 
-def test_dropin_backward_c1_fullsize(dev):
-    """The drop-in backward at HipGPT's default shape (B32 S256 E256 H8, the
-    single-read kernel) on unmasked probs, over the whole tensor: against the
-    oracle, and against the reference's own kernel on the same device
-    buffers where oracle/_ref is built."""
-    B, S, E, H = CONFIGS["c1"]
+@pytest.mark.parametrize("cfg", list(CONFIGS))
+def test_dropin_backward_fullsize(dev, cfg):
+    """The drop-in backward at the c1 (HipGPT's default, D = 32) and c2
+    (D = 64) shapes, both on the single-read per-(b, h) kernels, on unmasked
+    probs over the whole tensor: against the oracle, and against the
+    reference's own kernel on the same device buffers where oracle/_ref is
+    built."""
+    B, S, E, H = CONFIGS[cfg]
     qkv, go, probs = _inputs(B, S, E, H, causal=False, seed=23)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
@@ -218,3 +220,34 @@ def test_per_bh_backward_ragged_tail_stays_in_bounds(dev, B, S, E, H, causal):
     got2 = host(g2)
     assert np.isfinite(got2).all()
     assert np.abs(got2 - want).max() <= tol(want)
+
+
+D64_SHAPES = [(1, 1, 64, 1), (2, 7, 128, 2), (1, 32, 64, 1), (3, 44, 256, 4), (2, 100, 128, 2),
+              (1, 128, 512, 8), (2, 200, 192, 3), (2, 236, 128, 2), (1, 256, 128, 2)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,S,E,H", D64_SHAPES)
+def test_per_bh_d64_backward(dev, B, S, E, H, causal):
+    """D = 64 with S <= 256 runs the one-workgroup-per-(b, h) single-read
+    kernel, unmasked (the drop-in) and causal (the extended entry point),
+    from 1 to 8 key tiles, ragged tails included.  As in the D = 32 ragged
+    test, NaN sits directly after the probs inside the same allocation, so a
+    P load past the last (b, h)'s row S-1 would poison dK / dV, and a dQ
+    store past row S-1 would overwrite the next batch's rows."""
+    qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=17)
+    want = O.mha_backward(go, qkv, probs, B, S, E, H)
+    n = probs.size
+    pbuf = torch.full((n + 64 * S,), float("nan"), device=dev)
+    pbuf[:n] = dev_t(probs.reshape(-1))
+    d_p = pbuf[:n]
+    d_qkv, d_go = dev_t(qkv), dev_t(go)
+    d_g = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    if causal:
+        ws = torch.empty(B * H * S, device=dev)
+        A.attention_backward(d_go, d_qkv, d_p, d_g, B, S, E, H, causal=True, workspace=ws)
+    else:
+        A.launch_multihead_attention_backward(d_go, d_qkv, d_p, d_g, B, S, E, H)
+    got = host(d_g)
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= tol(want)
