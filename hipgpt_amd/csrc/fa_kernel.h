@@ -32,8 +32,8 @@ namespace fa {
 
 // Start stagger of short causal grids (see FaKernel::run): 35 ticks of the
 // 100 MHz s_memrealtime counter = 350 ns per launch rank, for grids of at
-// most 4 query blocks per (batch, head) that fill at least half of the
-// device's resident workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
+// most 4 query blocks per (batch, head) that are resident at once and fill
+// at least half of the device's workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
 // measured over 100 .. 800 ns per rank).
 constexpr unsigned long long kStaggerTicks = 35;
 // The same for grids that write probs: 1 us per rank without a causal mask
@@ -41,7 +41,10 @@ constexpr unsigned long long kStaggerTicks = 35;
 // 24.7 us); measured over 0.4 .. 1.6 us per rank.
 constexpr unsigned long long kStaggerTicksProbs = 100;
 constexpr unsigned long long kStaggerTicksProbsCausal = 70;
-constexpr int kStaggerMaxBlocks = 4;
+#ifndef HIPGPT_FA_STAGGER_MAX_BLOCKS
+#define HIPGPT_FA_STAGGER_MAX_BLOCKS 4
+#endif
+constexpr int kStaggerMaxBlocks = HIPGPT_FA_STAGGER_MAX_BLOCKS;  // 0: no start stagger
 
 // Compile-time loop over I = 0 .. N-1 (each body sees I as a constant).
 template <class F, int... Is>
@@ -211,9 +214,11 @@ struct FaKernel {
         // probs stores (the second sweep, HBM-bound) overlap the next rank's
         // score sweep (MFMA-bound) instead of every workgroup storing at once.
         // Only the workgroups the device starts together (block ids below
-        // stagger_slots, set by the launcher when the grid fills at least half
-        // of the resident slots) are delayed: a small grid has no burst to
-        // spread, and later workgroups of a large grid start as slots free up.
+        // stagger_slots, set by the launcher when the whole grid is resident at
+        // once and fills at least half of the slots) are delayed: a small grid
+        // has no burst to spread, and a grid larger than the device starts its
+        // later workgroups as slots free up (B = 128 measured the same with and
+        // without the stagger).
         if ((CAUSAL || PROBS) && rank > 0 && (int)blockIdx.x < a.stagger_slots) {
             const unsigned long long ticks = PROBS ? (CAUSAL ? kStaggerTicksProbsCausal : kStaggerTicksProbs) : kStaggerTicks;
             const unsigned long long t_end = __builtin_amdgcn_s_memrealtime() + (unsigned long long)rank * ticks;
@@ -562,7 +567,8 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     if ((CAUSAL || PROBS) && args.n_qblk > 1 && args.n_qblk <= kStaggerMaxBlocks) {
         static ResidentSlots cache;
         const int slots = cache.get(reinterpret_cast<const void*>(kern), NQS * NKS * 64, 0);
-        if (slots > 0 && 2 * grid >= slots) args.stagger_slots = slots;
+        // only grids the device holds at once, filling at least half of it
+        if (slots > 0 && 2 * grid >= slots && grid <= slots) args.stagger_slots = slots;
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), 0, stream, args);
     return hipGetLastError();
