@@ -585,6 +585,9 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
 #ifndef HIPGPT_SCORE_SPILL
 #define HIPGPT_SCORE_SPILL 1
 #endif
+#ifndef HIPGPT_SCORE_SPILL_MIN_DP
+#define HIPGPT_SCORE_SPILL_MIN_DP 128
+#endif
 
 // Score-resident stages of a traits type (PROBS_RES_STAGES; 0 = the probs
 // sweeps recompute Q K^T).
@@ -598,7 +601,7 @@ struct probs_res_stages<TR, std::void_t<decltype(TR::PROBS_RES_STAGES)>> {
 template <class TR, int NQS, int NKS, int PF, bool VEC>
 hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
     constexpr int SRT = probs_res_stages<TR>::value;
-    constexpr bool kSpill = HIPGPT_SCORE_SPILL && VEC && sizeof(typename TR::elem) == 4 && TR::DP >= 128;
+    constexpr bool kSpill = HIPGPT_SCORE_SPILL && VEC && sizeof(typename TR::elem) == 4 && TR::DP >= HIPGPT_SCORE_SPILL_MIN_DP;
     if constexpr (SRT > 0) {
         // every wave's key tiles fit the resident stages (Sk <= SRT * NKS * 32)
         if (probs && ((a.Sk + BK - 1) / BK + NKS - 1) / NKS <= SRT)
