@@ -64,7 +64,7 @@ CONFIGS = {
     "c5": (64, 12, 1, 2048, 64, False, "f32", False, "decode"),
     # c5 as a KV-cache step: 2047 cached rows + the new one appended in place
     "c5_kvcache": (64, 12, 1, 2048, 64, False, "f32", False, "kvcache"),
-    # One long sequence: few (b, h) rows, so the keys are split over 32
+    # One long sequence: few (b, h) rows, so the keys are split over 64
     # workgroups per row and the reduce kernel merges them.
     "decode_long": (1, 12, 1, 32768, 64, False, "f32", False, "decode"),
     # The c1 head shape at other batch sizes: HipGPT's generation call
