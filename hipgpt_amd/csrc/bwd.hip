@@ -340,7 +340,7 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
         if (bwd::bh_ok(a)) return bwd::launch_bh(a, s);
-        if (bwd::bh_probs64_ok(a)) return bwd::launch_bh_probs64(a, s);
+        if (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a)) return bwd::launch_bh64(a, s);
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
         return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);

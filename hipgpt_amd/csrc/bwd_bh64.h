@@ -1,7 +1,8 @@
-// bwd_bh64.h -- stored-probs attention backward for head dim 64 and S <= 256
-// with one workgroup per (b, h), every P tile read from memory once: HipGPT's
-// drop-in backward (src/hip_kernels.cpp:1159-1272) at E / H = 64 (the c2
-// shape, E = 512, H = 8), and the causal extended call.
+// bwd_bh64.h -- attention backward for head dim 64 and S <= 256 with one
+// workgroup per (b, h): with stored probs, every P tile read from memory once
+// (HipGPT's drop-in backward, src/hip_kernels.cpp:1159-1272, at E / H = 64 --
+// the c2 shape, E = 512, H = 8 -- and the causal extended call), or from the
+// forward's O and row log-sum-exp with P rebuilt (the probs-free pair).
 //
 // The step structure follows bwd_bh_probs_kernel (bwd_bh.h): at step t every
 // wave works on query tile t against its own key tile j (K_j and V_j in
@@ -18,6 +19,15 @@
 // steps t < j and loads no P above the diagonal; every wave's partial-sum
 // and dQ-term slots start at zero, so the fixed-order sums need no masks.
 // All summation orders are fixed: results are deterministic.
+//
+// LSE (probs-free): Dq_i = dO_i . O_i needs no sweep over the keys, so each
+// wave computes it, with lse' = lse log2 e, for the rows of its own query
+// tile into an LDS table before the first step; no partial sums are formed.
+// Each step rebuilds P = exp2(S' - lse') from S' = (c log2 e) Q K^T (K
+// pre-scaled in registers; masks on the causal diagonal and on keys past S
+// only), the S' and dP chains starting from -lse' and -Dq, so P = exp2(S'
+// chain) and dS = P * (dP chain).  160 MFMAs per wave and step; the
+// mid-step barrier only orders the single buffer of dQ terms.
 #pragma once
 
 #include "bwd_bh.h"
@@ -38,18 +48,19 @@ constexpr int PPd = DK + 8;     // pitch of a dQ term's rows: rows q and q+4 on 
 // immediate offsets reach 64 KB only)
 constexpr int XS = 0;                        // per-wave scratch [NW][BK][XP]
 constexpr int RING = XS + NW * BK * XP;
-constexpr int PD = RING + SLOTS * 2 * TILE;  // partial row sums [2][NW][BK]
+constexpr int PD = RING + SLOTS * 2 * TILE;  // partial row sums [2][NW][BK]; LSE: lse' and Dq [2][MAXS]
 constexpr int DQP = PD + 2 * NW * BK;        // dQ terms [NW][BK][PPd]
 constexpr int TOTAL = DQP + NW * BK * PPd;
 constexpr int kLdsBytes = TOTAL * 4;
 constexpr int DQCOL = BK;  // the step's Dq in the scratch rows' pitch padding
 static_assert(XP >= BK + 4, "room for the step's Dq in the scratch pitch");
+static_assert(NW * BK == MAXS, "the LSE mode's lse' and Dq tables fit the partial-sum slots");
 static_assert(kLdsBytes <= 160 * 1024, "LDS of the D = 64 single-read kernel");
 static_assert(BK * CPRd == NW * 64, "one 16-byte chunk of each of Q and dO per thread and tile");
 }  // namespace p64
 
-template <bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
+template <bool CAUSAL, bool LSE>
+__global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
     using namespace p64;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -87,14 +98,16 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
     };
 
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(a.probs) + (int64_t)bhi * S * S, 0, S * S * 4, kBufferFlags);
+        LSE ? nullptr : const_cast<float*>(a.probs) + (int64_t)bhi * S * S, 0, LSE ? 0 : S * S * 4, kBufferFlags);
 
     // The wave's keys: V (B operand of dP, lane (c, h) holding dims
-    // 32h .. 32h+31 of key kj) and K as the B operand of the dQ product over
-    // keys (block n, step s: key dq_key(s, h), dim 32n + c), read back through
-    // the scratch.  Only what the first step needs is requested before it.
-    float vr[DK / 2], kq[NB][16];
-    floatx16 p, pn;  // P of the step's query tile and of the next one
+    // 32h .. 32h+31 of key kj), with LSE also K pre-scaled by c log2 e (B
+    // operand of S', the same layout), and K as the B operand of the dQ
+    // product over keys (block n, step s: key dq_key(s, h), dim 32n + c),
+    // read back through the scratch.  Only what the first step needs is
+    // requested before it.
+    float vr[DK / 2], kq[NB][16], kr[LSE ? DK / 2 : 1];
+    floatx16 p, pn;  // stored probs: P of the step's query tile and of the next one
     const Stage r0 = ring_load(0);
     Stage rn = ring_load(1);
     floatx4 kv[DK / 8], vv[DK / 8];
@@ -104,14 +117,40 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
     if (active) {
 #pragma unroll
         for (int s = 0; s < DK / 8; ++s) vv[s] = vl.load(kj, hf * (DK / 8) + s);
-        if (meets(0)) load_p_tile(p, pr, 0, kj, kval, hf, S);
+        if (!LSE && meets(0)) load_p_tile(p, pr, 0, kj, kval, hf, S);
 #pragma unroll
         for (int s = 0; s < DK / 8; ++s) kv[s] = kl.load(kj, hf * (DK / 8) + s);
     }
     ring_store(0, r0);
-    // every wave's partial-sum and dQ-term slots start at zero: waves past the
-    // last key tile, and causally before their diagonal, leave them so
-    lds[PD + (hf * NW + wave) * BK + c] = 0.f;
+    if constexpr (LSE) {
+        // the rows of query tile `wave`: lse' = lse log2 e (+inf past S, so P
+        // = 0 there) and Dq = dO . O, lane (c, h) summing dims 32h .. 32h+31
+        // of row c; tables [S] at PD (lse') and PD + MAXS (Dq)
+        if (active) {
+            RowLoader ol, gl;
+            ol.init(a.o + base, a.ts, S, DK);
+            gl.init(a.go + base, a.ts, S, DK);
+            const int row = wave * BK + c;
+            const float lsev = row < S ? a.lse[(int64_t)bhi * S + row] : 0.f;
+            float d = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < DK / 8; ++s2) {
+                const floatx4 o4 = ol.load(row, hf * (DK / 8) + s2), g4 = gl.load(row, hf * (DK / 8) + s2);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d = fmaf(g4[e], o4[e], d);
+            }
+            d += __shfl_xor(d, 32);
+            if (hf == 0) {
+                lds[PD + row] = row < S ? lsev * kLog2e : kInf;
+                lds[PD + MAXS + row] = d;
+            }
+        }
+    } else {
+        // every wave's partial-sum slots start at zero: waves past the last
+        // key tile, and causally before their diagonal, leave them so
+        lds[PD + (hf * NW + wave) * BK + c] = 0.f;
+    }
+    // the same for the dQ-term slots
 #pragma unroll
     for (int k = 0; k < BK * (DK / 4) / 64; ++k) {
         const int f = lane + 64 * k;  // [row][chunk of four dims]
@@ -194,8 +233,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
 #pragma unroll
         for (int s = 0; s < DK / 8; ++s)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) vr[4 * s + j] = vv[s][j];
-        if (nt > 1 && meets(1)) load_p_tile(pn, pr, 1, kj, kval, hf, S);
+            for (int j = 0; j < 4; ++j) {
+                vr[4 * s + j] = vv[s][j];
+                if constexpr (LSE) kr[4 * s + j] = kv[s][j] * (a.scale * kLog2e);
+            }
+        if (!LSE && nt > 1 && meets(1)) load_p_tile(pn, pr, 1, kj, kval, hf, S);
         // K through the scratch, one 32-dim block at a time: lanes of half n
         // hold dims 32n .. 32n+31.  The lanes of the other half read what
         // these lanes wrote: a wave's LDS accesses run in order, and the
@@ -212,73 +254,155 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
         }
     }
 
-    // Step t (t % 2 == PAR) of every wave: pc holds P of tile t, pnx P of
-    // tile t+1 (requested a step ago); P of tile t+2 goes into pc once dS is
-    // formed, so the two buffers alternate roles and nothing is copied.
+    // A chain over the head dim: acc[m = row c of `rt`][n = key c] += sum_d
+    // rt[c][d] bv[d], lane (c, h) taking d = 32h .. 32h+31 (16 at a time).
+    auto chain = [&](const float* rt, const float (&bv)[DK / 2], floatx16 acc) {
+        const float* rr = rt + c * RPd + hf * (DK / 2);
+#pragma unroll
+        for (int hb = 0; hb < DK / 32; ++hb) {
+            floatx4 dv[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dv[j] = *reinterpret_cast<const floatx4*>(rr + 16 * hb + 4 * j);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(dv[k >> 2][k & 3], bv[16 * hb + k], acc, 0, 0, 0);
+        }
+        return acc;
+    };
+    // dV^T += dO^T P: A[d][query] read from the row-major dO tile
+    auto grad_v = [&](const float* gt, const floatx16& pv) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                accv[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[acc_key(r, hf) * RPd + 32 * n + c], pv[r], accv[n], 0, 0, 0);
+    };
+    // dK^T += Q^T dS, then the dQ term dS K: dS^T through the scratch
+    // ([key][query]), one 32-dim block at a time, each stored as it completes
+    // (register r <-> query acc_key(r, h), lane <-> dim 32n + c)
+    auto grad_kq = [&](const float* qt, const floatx16& ds) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acck[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[acc_key(r, hf) * RPd + 32 * n + c], ds[r], acck[n], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) = floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            floatx16 aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(0, hf) * XP + c], kq[n][0], floatx16{}, 0, 0, 0);
+#pragma unroll
+            for (int s = 1; s < 16; ++s)
+                aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[n][s], aq, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dqw[(8 * (r >> 2) + (r & 3)) * PPd + 32 * n] = aq[r];
+        }
+    };
+    const bool kedge = wave * BK + BK > S;  // keys past S in this wave's tile
+
+    // Step t (t % 2 == PAR) of every wave.  Stored probs: pc holds P of tile
+    // t, the other buffer P of tile t+1 (requested a step ago); P of tile t+2
+    // goes into pc once dS is formed, so the two buffers alternate roles and
+    // nothing is copied.  LSE: P is rebuilt, pc unused.
     auto step = [&](auto par_tag, int t, floatx16& pc) {
         constexpr int PAR = decltype(par_tag)::value;
         const bool cur = meets(t);
         const float* qt = slot(t);
         const float* gt = qt + TILE;
-        // the dQ rows of tile t-1 (its terms were published by the last
-        // barrier), then dP of tile t and its partial row sums
+        // the dQ rows of tile t-1 (its terms were published by the last barrier)
         if (t > 0) reduce_dq(t - 1);
-        floatx16 dp;
-        if (cur) {
-            dp = dp_tile(gt);
-            partial(std::integral_constant<int, PAR>{}, pc, dp);
-        }
-        lds_barrier();  // the partial sums of tile t; every wave has read the dQ terms of tile t-1
-        if (cur) {
-            // Dq of query tile t (lane: query c): the partials in key-tile
-            // order, kept in the scratch's padding for the register-order reads
-            float dsum = 0.f;
+        if constexpr (LSE) {
+            lds_barrier();  // every wave has read the dQ terms of tile t-1
+            if (cur) {
+                // S' - lse' and dP - Dq, register r <-> query t*32 + acc_key(r, h), lane <-> key
+                floatx16 sc, dpc;
 #pragma unroll
-            for (int v = 0; v < NW; ++v) dsum += pdl[(PAR * NW + v) * BK];
-            if (hf == 0) X[(c >> 2) * XP + DQCOL + (c & 3)] = dsum;
-            asm volatile("" ::: "memory");
-            // dV^T += dO^T P: A[d][query] read from the row-major dO tile
+                for (int g = 0; g < 4; ++g) {
+                    const floatx4 l4 = *reinterpret_cast<const floatx4*>(lds + PD + t * BK + 8 * g + 4 * hf);
+                    const floatx4 d4 = *reinterpret_cast<const floatx4*>(lds + PD + MAXS + t * BK + 8 * g + 4 * hf);
 #pragma unroll
-            for (int n = 0; n < NB; ++n)
+                    for (int j = 0; j < 4; ++j) {
+                        sc[4 * g + j] = -l4[j];
+                        dpc[4 * g + j] = -d4[j];
+                    }
+                }
+                sc = chain(qt, kr, sc);
+                dpc = chain(gt, vr, dpc);
+                floatx16 pv, ds;
+                if (kedge || (CAUSAL && t == wave)) {  // keys past S, the causal diagonal
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    accv[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[acc_key(r, hf) * RPd + 32 * n + c], pc[r],
-                                                                   accv[n], 0, 0, 0);
-            floatx16 ds;
+                    for (int r = 0; r < 16; ++r) {
+                        const bool vis = kval && (!CAUSAL || kj <= t * BK + acc_key(r, hf));
+                        pv[r] = vis ? fast_exp2(sc[r]) : 0.f;
+                        ds[r] = pv[r] * dpc[r];
+                    }
+                } else {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const floatx4 d4 = *reinterpret_cast<const floatx4*>(X + (2 * g + hf) * XP + DQCOL);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) ds[4 * g + j] = pc[4 * g + j] * (dp[4 * g + j] - d4[j]);
+                    for (int r = 0; r < 16; ++r) {
+                        pv[r] = fast_exp2(sc[r]);
+                        ds[r] = pv[r] * dpc[r];
+                    }
+                }
+                grad_v(gt, pv);
+                grad_kq(qt, ds);
             }
-            if (t + 2 < nt) load_p_tile(pc, pr, t + 2, kj, kval, hf, S);
-            // dK^T += Q^T dS
-#pragma unroll
-            for (int n = 0; n < NB; ++n)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    acck[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[acc_key(r, hf) * RPd + 32 * n + c], ds[r],
-                                                                   acck[n], 0, 0, 0);
-            // dQ term dS K: dS^T through the scratch ([key][query]), one 32-dim
-            // block at a time, each stored as it completes (register r <->
-            // query acc_key(r, h), lane <-> dim 32n + c)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
-                    floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int n = 0; n < NB; ++n) {
-                floatx16 aq =
-                    __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(0, hf) * XP + c], kq[n][0], floatx16{}, 0, 0, 0);
-#pragma unroll
-                for (int s = 1; s < 16; ++s)
-                    aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[n][s], aq, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) dqw[(8 * (r >> 2) + (r & 3)) * PPd + 32 * n] = aq[r];
+        } else {
+            // dP of tile t and its partial row sums
+            floatx16 dp;
+            if (cur) {
+                dp = dp_tile(gt);
+                partial(std::integral_constant<int, PAR>{}, pc, dp);
             }
-        } else if (t + 2 < nt && meets(t + 2)) {
-            load_p_tile(pc, pr, t + 2, kj, kval, hf, S);  // causally: the wave's first tile
+            lds_barrier();  // the partial sums of tile t; every wave has read the dQ terms of tile t-1
+            if (cur) {
+                // Dq of query tile t (lane: query c): the partials in key-tile
+                // order, kept in the scratch's padding for the register-order reads
+                float dsum = 0.f;
+#pragma unroll
+                for (int v = 0; v < NW; ++v) dsum += pdl[(PAR * NW + v) * BK];
+                if (hf == 0) X[(c >> 2) * XP + DQCOL + (c & 3)] = dsum;
+                asm volatile("" ::: "memory");
+                // (written out here: through grad_v and grad_kq this branch
+                // spills two registers at 256 VGPRs)
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        accv[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(gt[acc_key(r, hf) * RPd + 32 * n + c], pc[r],
+                                                                       accv[n], 0, 0, 0);
+                floatx16 ds;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const floatx4 d4 = *reinterpret_cast<const floatx4*>(X + (2 * g + hf) * XP + DQCOL);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) ds[4 * g + j] = pc[4 * g + j] * (dp[4 * g + j] - d4[j]);
+                }
+                if (t + 2 < nt) load_p_tile(pc, pr, t + 2, kj, kval, hf, S);
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acck[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(qt[acc_key(r, hf) * RPd + 32 * n + c], ds[r],
+                                                                       acck[n], 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
+                        floatx4{ds[4 * g], ds[4 * g + 1], ds[4 * g + 2], ds[4 * g + 3]};
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int n = 0; n < NB; ++n) {
+                    floatx16 aq =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(0, hf) * XP + c], kq[n][0], floatx16{}, 0, 0, 0);
+#pragma unroll
+                    for (int s = 1; s < 16; ++s)
+                        aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[n][s], aq, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dqw[(8 * (r >> 2) + (r & 3)) * PPd + 32 * n] = aq[r];
+                }
+            } else if (t + 2 < nt && meets(t + 2)) {
+                load_p_tile(pc, pr, t + 2, kj, kval, hf, S);  // causally: the wave's first tile
+            }
         }
         ring_store(t + 1, rn);
         rn = ring_load(t + 2);
@@ -313,24 +437,33 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs64_kernel(BwdArgs a) {
 
 }  // namespace bh
 
-// Stored probs with D = 64 (causal or not), S <= 256, and the tiled kernels'
-// layout conditions (checked by the caller): P is read as single floats, so
-// there is no condition on S or on the probs' alignment.
+// D = 64 (causal or not), S <= 256, and the tiled kernels' layout conditions
+// (checked by the caller).  Stored probs are read as single floats, so there
+// is no condition on S or on the probs' alignment; without them the forward's
+// O and lse are required (the caller checks that too).
 #ifndef HIPGPT_BH_PROBS_D64
 #define HIPGPT_BH_PROBS_D64 1
+#endif
+#ifndef HIPGPT_BH_LSE_D64
+#define HIPGPT_BH_LSE_D64 1
 #endif
 inline bool bh_probs64_ok(const BwdArgs& a) {
     return HIPGPT_BH_PROBS_D64 && a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS;
 }
+inline bool bh_lse64_ok(const BwdArgs& a) {
+    return HIPGPT_BH_LSE_D64 && !a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS;
+}
 
-inline hipError_t launch_bh_probs64(const BwdArgs& a, hipStream_t s) {
+inline hipError_t launch_bh64(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    auto kern = a.causal ? bh::bwd_bh_probs64_kernel<true> : bh::bwd_bh_probs64_kernel<false>;
-    static std::atomic<unsigned long long> attr_set[2] = {{0}, {0}};
-    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(kern), bh::p64::kLdsBytes, attr_set[a.causal ? 1 : 0]);
+    const int mode = (a.causal ? 1 : 0) + (a.probs ? 0 : 2);
+    static void (*const kerns[4])(BwdArgs) = {bh::bwd_bh64_kernel<false, false>, bh::bwd_bh64_kernel<true, false>,
+                                              bh::bwd_bh64_kernel<false, true>, bh::bwd_bh64_kernel<true, true>};
+    static std::atomic<unsigned long long> attr_set[4] = {{0}, {0}, {0}, {0}};
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(kerns[mode]), bh::p64::kLdsBytes, attr_set[mode]);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bh::NW * 64), bh::p64::kLdsBytes, s, a);
+    hipLaunchKernelGGL(kerns[mode], dim3((unsigned)grid), dim3(bh::NW * 64), bh::p64::kLdsBytes, s, a);
     return hipGetLastError();
 }
 

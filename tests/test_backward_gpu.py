@@ -234,7 +234,9 @@ def test_per_bh_d64_backward(dev, B, S, E, H, causal):
     from 1 to 8 key tiles, ragged tails included.  As in the D = 32 ragged
     test, NaN sits directly after the probs inside the same allocation, so a
     P load past the last (b, h)'s row S-1 would poison dK / dV, and a dQ
-    store past row S-1 would overwrite the next batch's rows."""
+    store past row S-1 would overwrite the next batch's rows.  The same
+    kernel without probs (P rebuilt from the forward's O and lse) is checked
+    on the same inputs."""
     qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=17)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     n = probs.size
@@ -251,3 +253,12 @@ def test_per_bh_d64_backward(dev, B, S, E, H, causal):
     got = host(d_g)
     assert np.isfinite(got).all()
     assert np.abs(got - want).max() <= tol(want)
+
+    out = torch.empty((B * S, E), device=dev)
+    lse = torch.empty(B * H * S, device=dev)
+    A.fwd_lse_qkv_planar(d_qkv, out, lse, B, S, E, H, causal=causal)
+    g2 = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    A.bwd_lse_qkv_planar(d_go, d_qkv, out, lse, g2, B, S, E, H, causal=causal)
+    got2 = host(g2)
+    assert np.isfinite(got2).all()
+    assert np.abs(got2 - want).max() <= tol(want)

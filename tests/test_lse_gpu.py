@@ -60,11 +60,12 @@ def run_pair(qkv, go, B, S, E, H, causal):
 
 
 # D = 32 and 64; S below, on and across the 32-row tile and the 128-query
-# workgroup block; several heads and sequences.  D = 32 with S <= 256 runs the
-# one-workgroup-per-(b, h) kernel (S = 1, 7, 32, 45, 100, 255, 256), S = 257 the
-# query/key-stationary pair.
+# workgroup block; several heads and sequences.  S <= 256 runs the
+# one-workgroup-per-(b, h) kernels (D = 32: S = 1, 7, 32, 45, 100, 255, 256;
+# D = 64: S = 1, 33, 64, 130, 200, 256), S = 257 the query/key-stationary pair.
 SHAPES = [(1, 1, 32, 1), (2, 7, 64, 2), (1, 33, 128, 2), (2, 64, 256, 4), (1, 100, 128, 4), (2, 130, 64, 1),
           (1, 256, 512, 8), (3, 45, 256, 8), (2, 32, 64, 2), (1, 255, 128, 4), (2, 256, 64, 2), (1, 257, 64, 2),
+          (1, 1, 64, 1), (2, 200, 128, 2), (1, 257, 128, 2),
           (4, 64, 2560, 80)]  # B*H = 320 workgroups: more than one per CU
 
 
