@@ -8,6 +8,9 @@
 // exponentiated tile is directly the P^T operand of O^T = V^T P^T.
 #pragma once
 
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 
 namespace hipgpt {
@@ -15,6 +18,12 @@ namespace fa {
 
 constexpr int BK = 32;  // keys per tile
 constexpr int QW = 32;  // queries per wave
+
+// Compile-time loop over I = 0 .. N-1 (each body sees I as a constant).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
 
 // Rescale threshold of the online softmax (log2 units): the running max of a
 // row is only raised when a tile's max exceeds it by more than this, so the

@@ -35,7 +35,10 @@ namespace fa {
 // most 4 query blocks per (batch, head) that are resident at once and fill
 // at least half of the device's workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
 // measured over 100 .. 800 ns per rank).
-constexpr unsigned long long kStaggerTicks = 35;
+#ifndef HIPGPT_FA_STAGGER_TICKS
+#define HIPGPT_FA_STAGGER_TICKS 35
+#endif
+constexpr unsigned long long kStaggerTicks = HIPGPT_FA_STAGGER_TICKS;
 // The same for grids that write probs: 1 us per rank without a causal mask
 // (c1 drop-in 31.3 -> 29.9 us), 700 ns with one (c1 with probs 25.0 ->
 // 24.7 us); measured over 0.4 .. 1.6 us per rank.
@@ -45,12 +48,6 @@ constexpr unsigned long long kStaggerTicksProbsCausal = 70;
 #define HIPGPT_FA_STAGGER_MAX_BLOCKS 4
 #endif
 constexpr int kStaggerMaxBlocks = HIPGPT_FA_STAGGER_MAX_BLOCKS;  // 0: no start stagger
-
-// Compile-time loop over I = 0 .. N-1 (each body sees I as a constant).
-template <class F, int... Is>
-__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is...>) {
-    (f(std::integral_constant<int, Is>{}), ...);
-}
 
 // SRT > 0 (probs only): when a wave's key tiles span at most SRT stages, the
 // max/sum sweep keeps every score tile in registers and the probs sweep reads

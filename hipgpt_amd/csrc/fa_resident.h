@@ -19,7 +19,10 @@
 //     sub-blocks s and NQS-1-s (NQS = 8), and with NKS = 2 each sub-block's
 //     tiles alternate between two waves, so every SIMD carries the same
 //     causal work; the NKS partial (m, l, O) are merged in LDS at the end.
-//   * With probs the second sweep re-reads K/V from LDS (no reload).
+//   * With probs the second sweep re-reads K/V from LDS (no reload).  With
+//     one key split and at most 8 tiles (D = 64: the LDS holds no more), each
+//     wave keeps its masked score tiles in registers between the sweeps, so
+//     the probs sweep runs P V only instead of recomputing Q K^T.
 // The per-tile math (S^T = K Q^T, mask, online softmax, O^T += V^T P^T) is the
 // same as the streaming kernel's, through the same operand traits.
 #pragma once
@@ -35,6 +38,10 @@ namespace fa {
 
 // Largest LDS footprint a resident workgroup may use (bytes).
 constexpr int kResidentLdsMax = 152 * 1024;
+
+#ifndef HIPGPT_RES_SCORES
+#define HIPGPT_RES_SCORES 1
+#endif
 
 template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
 struct FaResident {
@@ -56,6 +63,10 @@ struct FaResident {
     static constexpr int ML_BYTES = NKS > 1 ? NW * 64 * 2 * 4 : 0;
     static constexpr int HEAD_BYTES = 256 + ML_BYTES;
     static constexpr int MERGE_BYTES = NKS > 1 ? NW * 64 * 16 * NDB * 4 : 0;
+    // Score tiles kept in registers between the probs sweeps (0: recomputed).
+    // The LDS bounds a wave's tiles: ceil(Sk / 32) <= MAX_TILES.
+    static constexpr int MAX_TILES = kResidentLdsMax / (TILE_ELEMS * (int)sizeof(E));
+    static constexpr int SRES = (HIPGPT_RES_SCORES && PROBS && NKS == 1 && MAX_TILES <= 8) ? MAX_TILES : 0;
 
     __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max,
                                                int* simd_slots) {
@@ -205,7 +216,9 @@ struct FaResident {
             for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(s[r], sc, -m_new));
             l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
             m_run = m_new;
+            return s;
         };
+        floatx16 sres[SRES > 0 ? SRES : 1];  // masked scores of tile t (SRES > 0)
 
         // ---- produce every tile, consume the ones this wave needs ----
         // Production runs L tiles ahead of consumption: tiles 0..L-1 are
@@ -223,7 +236,7 @@ struct FaResident {
                 if (t + L < T) issue(t + L, slot_tag);
             }
         };
-        auto step = [&](int t, auto slot_tag) {
+        auto step = [&](int t, auto slot_tag, auto consume) {
             if (t >= T) return;
             if (t + L < T) {
                 publish(t + L, slot_tag);
@@ -231,11 +244,14 @@ struct FaResident {
             }
             if (t < wtiles && t % NKS == ks) {
                 wait_tile(t);
-                if (PROBS)
-                    stats(t);
-                else
-                    online(t);
+                consume(t);
             }
+        };
+        auto consume = [&](int t) {
+            if (PROBS)
+                stats(t);
+            else
+                online(t);
         };
         if (0 < T) issue(0, S0{});
         if (1 < T) issue(1, S1{});
@@ -249,12 +265,22 @@ struct FaResident {
             ahead(2, S2{});
             ahead(3, S3{});
         }
-        for (int t0 = 0; t0 < T; t0 += L) {
-            step(t0, S0{});
-            step(t0 + 1, S1{});
-            if (L == 4) {
-                step(t0 + 2, S2{});
-                step(t0 + 3, S3{});
+        if constexpr (SRES > 0) {
+            // T <= SRES: every tile index is a compile-time constant
+            static_for(
+                [&](auto tc) {
+                    constexpr int TT = decltype(tc)::value;
+                    step(TT, std::integral_constant<int, TT % L>{}, [&](int t) { sres[TT] = stats(t); });
+                },
+                std::make_integer_sequence<int, (SRES > 0 ? SRES : 1)>{});
+        } else {
+            for (int t0 = 0; t0 < T; t0 += L) {
+                step(t0, S0{}, consume);
+                step(t0 + 1, S1{}, consume);
+                if (L == 4) {
+                    step(t0 + 2, S2{}, consume);
+                    step(t0 + 3, S3{}, consume);
+                }
             }
         }
 
@@ -280,14 +306,23 @@ struct FaResident {
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
             float* prow = probs_bh + (int64_t)qi * Sk;
             const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
-            for (int t = ks; t < wtiles; t += NKS) {
-                floatx16 s = scores(t);
+            auto probs_tile = [&](int t, floatx16 s) {
                 typename TR::VReg vreg;
                 TR::load_v(vreg, tiles + t * TILE_ELEMS + TR::KTILE, c, hf);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -mlog));
                 if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 TR::pv(vreg, s, o, c, hf);
+            };
+            if constexpr (SRES > 0) {
+                static_for(
+                    [&](auto tc) {
+                        constexpr int TT = decltype(tc)::value;
+                        if (TT < wtiles) probs_tile(TT, sres[TT]);
+                    },
+                    std::make_integer_sequence<int, (SRES > 0 ? SRES : 1)>{});
+            } else {
+                for (int t = ks; t < wtiles; t += NKS) probs_tile(t, scores(t));
             }
             if (CAUSAL && qw0 < Sq && ks == 0) zero_probs_tail(probs_bh, qw0, Sq, Sk, wtiles * BK, lane, pvec);
             l_run = 1.0f;
