@@ -28,7 +28,7 @@ namespace {
 
 using fa::BK;
 
-template <int DP_, bool VPRE_ = (DP_ <= 32)>
+template <int DP_, bool VPRE_ = (DP_ <= 32), int SRES_ = (DP_ == 32 ? 4 : 0)>
 struct F32Traits {
     static constexpr int DP = DP_;
     using elem = float;
@@ -115,9 +115,10 @@ struct F32Traits {
     // us; prefetching V under the same cap spills).
     static constexpr bool VPRE = VPRE_;
     static constexpr int WAVES_PER_EU = (DP == 64 && !VPRE) ? 4 : 1;
-    // With probs at DP = 32, rows of up to 4 stages (Sk <= 256 at two key
-    // splits) keep their score tiles in registers between the two sweeps.
-    static constexpr int PROBS_RES_STAGES = DP == 32 ? 4 : 0;
+    // With probs, rows of up to SRES stages keep their score tiles in
+    // registers between the two sweeps (DP = 32: 4 stages, Sk <= 256 at two
+    // key splits).
+    static constexpr int PROBS_RES_STAGES = SRES_;
     struct VReg {
         floatx4 v[VPRE ? DP / 32 : 1][4];
         const float* vt;
@@ -215,8 +216,43 @@ int fa_f32_padded_dim(int D) {
 #define HIPGPT_RES_D32_NKS 0
 #endif
 
+// Small D <= 32 problems (at most 128 query tiles of 32 rows in all, 128 to
+// 256 keys -- HipGPT's generation call, B = 1, H = 8, S = 256, is 64 tiles):
+// the 2 x 2 workgroups would put one or two waves on a few dozen SIMDs, so
+// each query sub-block is split over 4 waves instead (1 x 4, at most two
+// stages of key tiles each, scores kept in registers with probs).  The
+// generation call 12.6 -> 9.2 us, B = 1 causal 9.5 -> 7.5 us; from 256 query
+// tiles on the two shapes measure the same, and below 128 keys a split would
+// hold no tile.
+#ifndef HIPGPT_F32_SMALL
+#define HIPGPT_F32_SMALL 1
+#endif
+#ifndef HIPGPT_F32_SMALL_NQS
+#define HIPGPT_F32_SMALL_NQS 1
+#endif
+#ifndef HIPGPT_F32_SMALL_NKS
+#define HIPGPT_F32_SMALL_NKS 4
+#endif
+#ifndef HIPGPT_F32_SMALL_MAX_QTILES
+#define HIPGPT_F32_SMALL_MAX_QTILES 128
+#endif
+
 hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t stream) {
     const bool probs = a.probs != nullptr;
+#if HIPGPT_F32_SMALL
+    {
+        constexpr int NQ = HIPGPT_F32_SMALL_NQS, NK = HIPGPT_F32_SMALL_NKS, ST = 8 / NK;
+        using TS = F32Traits<32, true, ST>;
+        if (vec && fa_f32_padded_dim(a.D) == 32 && a.Sk >= 128 && a.Sk <= 256 &&
+            (int64_t)a.B * a.H * ((a.Sq + 31) / 32) <= HIPGPT_F32_SMALL_MAX_QTILES) {
+            if (probs)
+                return causal ? fa::launch_fa<TS, NQ, NK, 1, true, true, true, ST>(a, stream)
+                              : fa::launch_fa<TS, NQ, NK, 1, false, true, true, ST>(a, stream);
+            return causal ? fa::launch_fa<TS, NQ, NK, 1, true, false, true>(a, stream)
+                          : fa::launch_fa<TS, NQ, NK, 1, false, false, true>(a, stream);
+        }
+    }
+#endif
     if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ && !a.lse) {  // the resident kernel writes no lse
 #if HIPGPT_RES_D32_NKS > 0
         if (a.D == 32 && fa::resident_lds_bytes<F32Traits<32>, 8, HIPGPT_RES_D32_NKS>(a) != 0)

@@ -71,6 +71,25 @@ def test_planar_causal_matches_oracle(dev, B, S, E, H, causal, with_probs):
             assert np.all(p[:, :, iu[0], iu[1]] == 0.0)
 
 
+# D <= 32, 128..256 keys and at most 128 query tiles: the launcher splits each
+# query sub-block's keys over 4 waves (HipGPT's generation call, B = 1, H = 8,
+# S = 256, D = 32, is one such shape).  Padded D (16, 24), ragged S, both
+# masks, probs on and off.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_probs", [True, False])
+@pytest.mark.parametrize("B,S,E,H", [(1, 256, 256, 8), (2, 129, 64, 2), (1, 200, 96, 4), (2, 128, 32, 2),
+                                     (1, 250, 48, 2)])
+def test_small_grid_key_split_matches_oracle(dev, B, S, E, H, causal, with_probs):
+    qkv = O.seeded_planar(S * 17 + E + B, B, S, E)
+    want_o, want_p = O.launch_multihead_attention(qkv, B, S, E, H, causal=causal, want_probs=True)
+    d_out = torch.full((B * S, E), float("nan"), device=dev)
+    d_p = torch.full((B, H, S, S), float("nan"), device=dev) if with_probs else None
+    A.qkv_planar(dev_t(qkv), d_out, d_p, B, S, E, H, causal=causal)
+    assert np.abs(host(d_out) - want_o).max() <= TOL_O
+    if with_probs:
+        assert np.abs(host(d_p) - want_p).max() <= TOL_P
+
+
 def _ref_or_skip():
     if not O.ref_available():
         pytest.skip("reference build oracle/_ref missing")
