@@ -233,6 +233,18 @@ int fa_f32_padded_dim(int D) {
 #ifndef HIPGPT_F32_SMALL_NKS
 #define HIPGPT_F32_SMALL_NKS 4
 #endif
+// The same split at D = 64 replaces the resident kernel (one 8-wave
+// workgroup per (b, h), latency-bound when B*H is far below the CU count)
+// up to 512 query tiles: the generation call at E = 512 (B = 1, H = 8,
+// S = 256, drop-in) 47.1 -> 12.8 us, B = 8 drop-in 52.0 -> 26.9 us, B = 8
+// causal 29.8 -> 20.3 us; at B = 16 (1024 tiles) the causal resident kernel
+// is faster (31.0 against 38.7 us).
+#ifndef HIPGPT_F32_SMALL64
+#define HIPGPT_F32_SMALL64 1
+#endif
+#ifndef HIPGPT_F32_SMALL64_MAX_QTILES
+#define HIPGPT_F32_SMALL64_MAX_QTILES 512
+#endif
 #ifndef HIPGPT_F32_SMALL_MAX_QTILES
 #define HIPGPT_F32_SMALL_MAX_QTILES 128
 #endif
@@ -243,14 +255,26 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
     {
         constexpr int NQ = HIPGPT_F32_SMALL_NQS, NK = HIPGPT_F32_SMALL_NKS, ST = 8 / NK;
         using TS = F32Traits<32, true, ST>;
-        if (vec && fa_f32_padded_dim(a.D) == 32 && a.Sk >= 128 && a.Sk <= 256 &&
-            (int64_t)a.B * a.H * ((a.Sq + 31) / 32) <= HIPGPT_F32_SMALL_MAX_QTILES) {
+        const int64_t qtiles = (int64_t)a.B * a.H * ((a.Sq + 31) / 32);
+        const bool small = vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= HIPGPT_F32_SMALL_MAX_QTILES;
+        if (small && fa_f32_padded_dim(a.D) == 32) {
             if (probs)
                 return causal ? fa::launch_fa<TS, NQ, NK, 1, true, true, true, ST>(a, stream)
                               : fa::launch_fa<TS, NQ, NK, 1, false, true, true, ST>(a, stream);
             return causal ? fa::launch_fa<TS, NQ, NK, 1, true, false, true>(a, stream)
                           : fa::launch_fa<TS, NQ, NK, 1, false, false, true>(a, stream);
         }
+#if HIPGPT_F32_SMALL64
+        using T6 = F32Traits<64, true, ST>;
+        if (vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= HIPGPT_F32_SMALL64_MAX_QTILES &&
+            fa_f32_padded_dim(a.D) == 64) {
+            if (probs)
+                return causal ? fa::launch_fa<T6, NQ, NK, 1, true, true, true, ST>(a, stream)
+                              : fa::launch_fa<T6, NQ, NK, 1, false, true, true, ST>(a, stream);
+            return causal ? fa::launch_fa<T6, NQ, NK, 1, true, false, true>(a, stream)
+                          : fa::launch_fa<T6, NQ, NK, 1, false, false, true>(a, stream);
+        }
+#endif
     }
 #endif
     if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ && !a.lse) {  // the resident kernel writes no lse
