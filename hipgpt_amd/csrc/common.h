@@ -105,6 +105,17 @@ inline int device_resident_slots(const void* kern, int block, size_t lds) {
     return per_cu > 0 && cus > 0 ? per_cu * cus : 0;
 }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+inline int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int v = __atomic_load_n(&cus[dev], __ATOMIC_RELAXED);
+    if (v == 0 && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+        __atomic_store_n(&cus[dev], v, __ATOMIC_RELAXED);
+    return v;
+}
+
 // Per-device cache of device_resident_slots for one kernel (a static of the
 // launching template, so each kernel instantiation has its own).
 struct ResidentSlots {

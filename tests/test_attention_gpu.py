@@ -91,6 +91,22 @@ def test_small_grid_key_split_matches_oracle(dev, B, S, E, H, causal, with_probs
         assert np.abs(host(d_p) - want_p).max() <= TOL_P
 
 
+# D = 64 with S <= 256 and B*H at least the CU count (256 on MI355X): the
+# one-workgroup-per-(b, h) resident kernel, at ragged S.
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("with_probs", [True, False])
+@pytest.mark.parametrize("B,S,E,H", [(32, 200, 512, 8), (64, 130, 256, 4)])
+def test_resident_kernel_matches_oracle(dev, B, S, E, H, causal, with_probs):
+    qkv = O.seeded_planar(S * 19 + E + B, B, S, E)
+    want_o, want_p = O.launch_multihead_attention(qkv, B, S, E, H, causal=causal, want_probs=True)
+    d_out = torch.full((B * S, E), float("nan"), device=dev)
+    d_p = torch.full((B, H, S, S), float("nan"), device=dev) if with_probs else None
+    A.qkv_planar(dev_t(qkv), d_out, d_p, B, S, E, H, causal=causal)
+    assert np.abs(host(d_out) - want_o).max() <= TOL_O
+    if with_probs:
+        assert np.abs(host(d_p) - want_p).max() <= TOL_P
+
+
 def _ref_or_skip():
     if not O.ref_available():
         pytest.skip("reference build oracle/_ref missing")
