@@ -331,16 +331,28 @@ bool bwd_tiled_ok(const BwdArgs& a) {
            ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
 }
 
+// The one-workgroup-per-(b, h) kernels run a (b, h)'s steps in sequence, so
+// one (b, h) takes 30-80 us whatever the batch.  With causal stored probs (and
+// the D = 32 drop-in) they still beat the query-/key-stationary pair at any
+// batch; rebuilding P from lse, and the D = 64 drop-in, only once the (b, h)
+// pairs fill the CUs (S = 256, H = 8, B = 4: D = 64 from lse 83.2 -> 48.0 us,
+// D = 32 from lse 32.3 -> 27.5 us, D = 64 drop-in 84.4 -> 77.8 us with the
+// pair; B = 32 keeps the per-(b, h) kernels).
+static bool bh_enough(const BwdArgs& a) {
+    if (a.probs && (a.causal || a.D == 32)) return true;
+    return (int64_t)a.B * a.H >= device_cus();
+}
+
 bool bwd_uses_workspace(const BwdArgs& a) {
-    return a.probs && !(bwd_tiled_ok(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
+    return a.probs && !(bwd_tiled_ok(a) && bh_enough(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
 }
 
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     // recompute mode (no probs): tiled kernels only
     if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
-        if (bwd::bh_ok(a)) return bwd::launch_bh(a, s);
-        if (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a)) return bwd::launch_bh64(a, s);
+        if (bh_enough(a) && bwd::bh_ok(a)) return bwd::launch_bh(a, s);
+        if (bh_enough(a) && (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a))) return bwd::launch_bh64(a, s);
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
         return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);

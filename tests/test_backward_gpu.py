@@ -90,7 +90,9 @@ def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     one-workgroup-per-(b, h) kernels at 1, 2, 3, 5, 7 and 8 key tiles (odd
     counts leave a middle tile without a SIMD partner): causally the two-phase
     kernel, unmasked the single-read one, whose Dq sums P o dP instead of
-    dO . (P V) -- there the two agree to the tolerance."""
+    dO . (P V) -- there the two agree to the tolerance.  So do the D = 64
+    cases with S <= 256 and fewer (b, h) pairs than CUs: causally the
+    per-(b, h) kernel, unmasked the query-/key-stationary pair."""
     qkv, go, probs = _inputs(B, S, E, H, causal=True, seed=3)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
@@ -102,7 +104,9 @@ def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     got = host(g_c)
     assert np.abs(got - want).max() <= tol(want)
     per_bh = E // H == 32 and S % 4 == 0 and S <= 256
-    if E // H <= 128 and not per_bh:  # same MFMA kernels: skipped tiles contribute exact zeros
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    split64 = E // H == 64 and S <= 256 and B * H < cus
+    if E // H <= 128 and not per_bh and not split64:  # same MFMA kernels: skipped tiles contribute exact zeros
         assert np.array_equal(got, host(g_n))
     else:
         assert np.abs(got - host(g_n)).max() <= tol(want)
@@ -194,7 +198,9 @@ def test_per_bh_backward_ragged_tail_stays_in_bounds(dev, B, S, E, H, causal):
     the probs inside the same allocation, so a P load past the last (b, h)'s
     row S-1 would poison dK / dV; rows past S of one (b, h)'s dQ are the next
     batch's rows (or the dK plane), so a dQ store past S would overwrite
-    gradients.  Every element must be finite and match the oracle."""
+    gradients.  Every element must be finite and match the oracle.  (At
+    these batch sizes the probs-free pair runs the query-/key-stationary
+    kernels; the device-filling test below covers its per-(b, h) mode.)"""
     qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=13)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     n = probs.size
@@ -226,18 +232,13 @@ D64_SHAPES = [(1, 1, 64, 1), (2, 7, 128, 2), (1, 32, 64, 1), (3, 44, 256, 4), (2
               (1, 128, 512, 8), (2, 200, 192, 3), (2, 236, 128, 2), (1, 256, 128, 2)]
 
 
-@pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("B,S,E,H", D64_SHAPES)
-def test_per_bh_d64_backward(dev, B, S, E, H, causal):
-    """D = 64 with S <= 256 runs the one-workgroup-per-(b, h) single-read
-    kernel, unmasked (the drop-in) and causal (the extended entry point),
-    from 1 to 8 key tiles, ragged tails included.  As in the D = 32 ragged
-    test, NaN sits directly after the probs inside the same allocation, so a
-    P load past the last (b, h)'s row S-1 would poison dK / dV, and a dQ
-    store past row S-1 would overwrite the next batch's rows.  The same
-    kernel without probs (P rebuilt from the forward's O and lse) is checked
-    on the same inputs."""
-    qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=17)
+def _backward_both_modes(dev, B, S, E, H, causal, seed):
+    """The stored-probs backward (NaN directly after the probs inside the
+    same allocation, so a P load past the last (b, h)'s row S-1 would poison
+    dK / dV, and a dQ store past row S-1 would overwrite the next batch's
+    rows), then the probs-free pair on the same inputs, both against the
+    oracle."""
+    qkv, go, probs = _inputs(B, S, E, H, causal=causal, seed=seed)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     n = probs.size
     pbuf = torch.full((n + 64 * S,), float("nan"), device=dev)
@@ -262,3 +263,22 @@ def test_per_bh_d64_backward(dev, B, S, E, H, causal):
     got2 = host(g2)
     assert np.isfinite(got2).all()
     assert np.abs(got2 - want).max() <= tol(want)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,S,E,H", D64_SHAPES)
+def test_per_bh_d64_backward(dev, B, S, E, H, causal):
+    """D = 64 with S <= 256, from 1 to 8 key tiles, ragged tails included:
+    causal with stored probs runs the one-workgroup-per-(b, h) single-read
+    kernel; at these batch sizes (fewer (b, h) pairs than CUs) the drop-in
+    and the probs-free backward run the query-/key-stationary pair."""
+    _backward_both_modes(dev, B, S, E, H, causal, seed=17)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,S,E,H", [(32, 236, 256, 8), (32, 200, 512, 8)])
+def test_per_bh_backward_device_filling_batch(dev, B, S, E, H, causal):
+    """B*H = 256 (the CU count) at ragged S: every mode of the
+    one-workgroup-per-(b, h) kernels -- D = 32 and 64, drop-in, causal,
+    probs-free."""
+    _backward_both_modes(dev, B, S, E, H, causal, seed=23)
