@@ -44,6 +44,15 @@ constexpr unsigned long long kStaggerTicks = HIPGPT_FA_STAGGER_TICKS;
 // 24.7 us); measured over 0.4 .. 1.6 us per rank.
 constexpr unsigned long long kStaggerTicksProbs = 100;
 constexpr unsigned long long kStaggerTicksProbsCausal = 70;
+// Score-resident probs sweep: probs tiles stored through an LDS transpose as
+// whole 128-byte rows (1), non-temporal (2), or straight from the
+// accumulator layout, 32 bytes per row per instruction (0).  Measured
+// (cache-rotated / hot, us): c1 with probs 31.2 / 24.5 -> 28.6 / 24.6, the c1
+// drop-in 34.9 / 29.6 -> 33.1 / 30.0, B = 128 drop-in 138.7 / 124.2 ->
+// 124.7 / 111.2 with 2; 1 alone gained less rotated and lost hot.
+#ifndef HIPGPT_PROBS_TRANSPOSE
+#define HIPGPT_PROBS_TRANSPOSE 2
+#endif
 #ifndef HIPGPT_FA_STAGGER_MAX_BLOCKS
 #define HIPGPT_FA_STAGGER_MAX_BLOCKS 4
 #endif
@@ -359,6 +368,44 @@ struct FaKernel {
         // Score-resident probs sweeps (SRT > 0).  Stage I holds tile I*NKS + ks
         // of this wave; sres[I] keeps its masked scores between the sweeps.
         floatx16 sres[SRT > 0 ? SRT : 1];
+        // Probs stores of the score-resident sweep through LDS: the wave
+        // writes its P tile ([query][key], 16 keys per lane) into a private
+        // 32 x 36 scratch in the K half of the stage buffers (the probs sweep
+        // stages V only) and reads it back as 8 whole 128-byte rows per
+        // instruction, so every store writes full lines (non-temporal: the
+        // probs are not read again by this kernel).  The scratch is the
+        // wave's own: a memory clobber orders the exchange between its lanes.
+        constexpr bool kTransStore = HIPGPT_PROBS_TRANSPOSE && SRT > 0 && sizeof(E) == 4 && TR::KTILE >= QW * 36 &&
+                                     NW <= 2 * NKS;
+        auto store_probs_transposed = [&](float* prow0, const floatx16& p, int tb, bool pvec) {
+            float* const X = reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS + (wave % NKS) * TR::KTILE);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<floatx4*>(X + c * 36 + 8 * g + 4 * hf) =
+                    floatx4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
+            asm volatile("" ::: "memory");
+            const int rr = lane >> 3, cc = 4 * (lane & 7);
+            const bool full = pvec && tb + BK <= Sk;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int row = 8 * k + rr;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
+                if (qw0 + row < Sq) {
+                    float* dst = prow0 + (int64_t)row * Sk + tb + cc;
+                    if (full) {
+                        if (HIPGPT_PROBS_TRANSPOSE > 1)
+                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
+                        else
+                            *reinterpret_cast<floatx4*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (tb + cc + j < Sk) dst[j] = v[j];
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");  // the next tile's writes come after these reads
+        };
         auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
             if (nstages > 0) {
@@ -389,7 +436,11 @@ struct FaKernel {
                                 floatx16 p = sres[I];
 #pragma unroll
                                 for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -mlog));
-                                if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
+                                if constexpr (kTransStore) {
+                                    store_probs_transposed(prow - (int64_t)c * Sk, p, t * BK, pvec);
+                                } else {
+                                    if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
+                                }
                                 TR::pv(vreg, p, o, c, hf);
                             }
                         }
