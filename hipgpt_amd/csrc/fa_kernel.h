@@ -53,6 +53,12 @@ constexpr unsigned long long kStaggerTicksProbsCausal = 70;
 #ifndef HIPGPT_PROBS_TRANSPOSE
 #define HIPGPT_PROBS_TRANSPOSE 2
 #endif
+#ifndef HIPGPT_PROBS_TRANSPOSE_MIN_DP
+#define HIPGPT_PROBS_TRANSPOSE_MIN_DP 128
+#endif
+#ifndef HIPGPT_SPILL_NT
+#define HIPGPT_SPILL_NT 1
+#endif
 #ifndef HIPGPT_FA_STAGGER_MAX_BLOCKS
 #define HIPGPT_FA_STAGGER_MAX_BLOCKS 4
 #endif
@@ -80,8 +86,20 @@ struct FaKernel {
     // merge reuses the same memory.
     static constexpr int STAGE_ELEMS = NKS * (TR::KTILE + TR::VTILE);
     static constexpr int STAGE_BYTES = STAGE_ELEMS * (int)sizeof(E);
-    static constexpr int MERGE_BYTES = NW * 64 * (16 * NDB + 2) * 4;
-    static constexpr int LDS_BYTES = (2 * STAGE_BYTES > MERGE_BYTES) ? 2 * STAGE_BYTES : MERGE_BYTES;
+    static constexpr int MERGE_BYTES = NKS > 1 ? NW * 64 * (16 * NDB + 2) * 4 : 0;  // key-split merge only
+    static constexpr int BASE_BYTES = (2 * STAGE_BYTES > MERGE_BYTES) ? 2 * STAGE_BYTES : MERGE_BYTES;
+    // Probs stores through a per-wave LDS transpose (see store_t): the score-
+    // resident sweep borrows the idle K half of the stage buffers; the causal
+    // probs sweeps at padded D >= HIPGPT_PROBS_TRANSPOSE_MIN_DP (one workgroup
+    // per CU, LDS to spare) get a region of their own after BASE_BYTES, for
+    // the spilled scores and the probs alike (B4 H16 S2048 D128 with probs
+    // 880 -> 867 us).  Unmasked there, the transpose measured slower (the
+    // drop-in 1391 -> 1465 us).
+    static constexpr bool TRANS_RES = HIPGPT_PROBS_TRANSPOSE && SRT > 0 && sizeof(E) == 4 &&
+                                      TR::KTILE >= QW * 36 && NW <= 2 * NKS;
+    static constexpr bool TRANS_OWN = HIPGPT_PROBS_TRANSPOSE && PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 &&
+                                      DP >= HIPGPT_PROBS_TRANSPOSE_MIN_DP;
+    static constexpr int LDS_BYTES = BASE_BYTES + (TRANS_OWN ? NW * QW * 36 * 4 : 0);
 
     // Global -> register staging of one stage (K and V), 16-byte chunks.
     static constexpr int EPC = 16 / (int)sizeof(E);      // elements per chunk
@@ -280,6 +298,42 @@ struct FaKernel {
             }
             return s;
         };
+        // Probs stores through LDS: the wave writes its tile ([query][key], 16
+        // keys per lane in the accumulator layout) into a private 32 x 36
+        // scratch X and reads it back as 8 whole 128-byte rows per
+        // instruction, so every store writes full lines (optionally
+        // non-temporal).  X is the wave's own: a memory clobber orders the
+        // exchange between its lanes.  prow0: row qw0 of the probs.
+        auto store_t = [&](float* X, float* prow0, const floatx16& p, int tb, bool pvec, bool nt) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<floatx4*>(X + c * 36 + 8 * g + 4 * hf) =
+                    floatx4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
+            asm volatile("" ::: "memory");
+            const int rr = lane >> 3, cc = 4 * (lane & 7);
+            const bool full = pvec && tb + BK <= Sk;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int row = 8 * k + rr;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
+                if (qw0 + row < Sq) {
+                    float* dst = prow0 + (int64_t)row * Sk + tb + cc;
+                    if (full) {
+                        if (nt)
+                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
+                        else
+                            *reinterpret_cast<floatx4*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (tb + cc + j < Sk) dst[j] = v[j];
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");  // the next tile's writes come after these reads
+        };
+        float* const Xown = reinterpret_cast<float*>(lds_raw + BASE_BYTES) + wave * QW * 36;
+
         // ------------------------------------------------------------------
         // One stage of compute on LDS buffer (i & 1).  MODE 0: online softmax
         // + PV.  MODE 1: max/sum only (SPILL: and the scores stored).  MODE 2:
@@ -322,7 +376,10 @@ struct FaKernel {
                 l_run += ls;  // this lane half's partial; the halves are summed after the sweep
                 TR::pv(vreg, s, o, c, hf);
             } else if (MODE == 1) {
-                if (SPILL && qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
+                if constexpr (SPILL && TRANS_OWN)
+                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec, HIPGPT_SPILL_NT);
+                else if (SPILL && qi < Sq)
+                    store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 const float m_new = vmax(m_run, tile_max(s) * sc);
                 float ls = 0.f;
 #pragma unroll
@@ -332,7 +389,10 @@ struct FaKernel {
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -mlog));
-                if (qi < Sq) store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
+                if constexpr (TRANS_OWN)
+                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec, HIPGPT_PROBS_TRANSPOSE > 1);
+                else if (qi < Sq)
+                    store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 TR::pv(vreg, s, o, c, hf);
             }
         };
@@ -368,44 +428,6 @@ struct FaKernel {
         // Score-resident probs sweeps (SRT > 0).  Stage I holds tile I*NKS + ks
         // of this wave; sres[I] keeps its masked scores between the sweeps.
         floatx16 sres[SRT > 0 ? SRT : 1];
-        // Probs stores of the score-resident sweep through LDS: the wave
-        // writes its P tile ([query][key], 16 keys per lane) into a private
-        // 32 x 36 scratch in the K half of the stage buffers (the probs sweep
-        // stages V only) and reads it back as 8 whole 128-byte rows per
-        // instruction, so every store writes full lines (non-temporal: the
-        // probs are not read again by this kernel).  The scratch is the
-        // wave's own: a memory clobber orders the exchange between its lanes.
-        constexpr bool kTransStore = HIPGPT_PROBS_TRANSPOSE && SRT > 0 && sizeof(E) == 4 && TR::KTILE >= QW * 36 &&
-                                     NW <= 2 * NKS;
-        auto store_probs_transposed = [&](float* prow0, const floatx16& p, int tb, bool pvec) {
-            float* const X = reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS + (wave % NKS) * TR::KTILE);
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<floatx4*>(X + c * 36 + 8 * g + 4 * hf) =
-                    floatx4{p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3]};
-            asm volatile("" ::: "memory");
-            const int rr = lane >> 3, cc = 4 * (lane & 7);
-            const bool full = pvec && tb + BK <= Sk;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int row = 8 * k + rr;
-                const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
-                if (qw0 + row < Sq) {
-                    float* dst = prow0 + (int64_t)row * Sk + tb + cc;
-                    if (full) {
-                        if (HIPGPT_PROBS_TRANSPOSE > 1)
-                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
-                        else
-                            *reinterpret_cast<floatx4*>(dst) = v;
-                    } else {
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            if (tb + cc + j < Sk) dst[j] = v[j];
-                    }
-                }
-            }
-            asm volatile("" ::: "memory");  // the next tile's writes come after these reads
-        };
         auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
             if (nstages > 0) {
@@ -436,8 +458,10 @@ struct FaKernel {
                                 floatx16 p = sres[I];
 #pragma unroll
                                 for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -mlog));
-                                if constexpr (kTransStore) {
-                                    store_probs_transposed(prow - (int64_t)c * Sk, p, t * BK, pvec);
+                                if constexpr (TRANS_RES) {
+                                    float* const X = reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS +
+                                                                              (wave % NKS) * TR::KTILE);
+                                    store_t(X, prow - (int64_t)c * Sk, p, t * BK, pvec, HIPGPT_PROBS_TRANSPOSE > 1);
                                 } else {
                                     if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
                                 }
