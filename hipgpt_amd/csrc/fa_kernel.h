@@ -53,6 +53,14 @@ constexpr unsigned long long kStaggerTicksProbsCausal = 70;
 #ifndef HIPGPT_PROBS_TRANSPOSE
 #define HIPGPT_PROBS_TRANSPOSE 2
 #endif
+// O stores of the streaming kernel through a per-wave LDS transpose, as whole
+// rows of the head: plain (1) or non-temporal (2).  With 2, c1 17.85 -> 16.84 us
+// (cache-rotated; hot 15.77 -> 14.95), the c1 drop-in 33.2 -> 31.4 us; 1 alone
+// measured level, and non-temporal stores of the accumulator layout's 32-byte
+// row pieces were slower (c1 17.6 us).
+#ifndef HIPGPT_O_TRANSPOSE
+#define HIPGPT_O_TRANSPOSE 2
+#endif
 #ifndef HIPGPT_PROBS_TRANSPOSE_MIN_DP
 #define HIPGPT_PROBS_TRANSPOSE_MIN_DP 128
 #endif
@@ -100,6 +108,11 @@ struct FaKernel {
     static constexpr bool TRANS_OWN = HIPGPT_PROBS_TRANSPOSE && PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 &&
                                       DP >= HIPGPT_PROBS_TRANSPOSE_MIN_DP;
     static constexpr int LDS_BYTES = BASE_BYTES + (TRANS_OWN ? NW * QW * 36 * 4 : 0);
+    // O stores through LDS (whole rows of the head per lane group) where the
+    // per-wave scratch fits past the merge area within the LDS already used;
+    // only with 16-byte rows of the full padded head (VEC, D = DP).
+    static constexpr bool O_TRANS = HIPGPT_O_TRANSPOSE && VEC && sizeof(E) == 4 && DP <= 64 &&
+                                    MERGE_BYTES + NQS * QW * (DP + 4) * 4 <= BASE_BYTES;
 
     // Global -> register staging of one stage (K and V), 16-byte chunks.
     static constexpr int EPC = 16 / (int)sizeof(E);      // elements per chunk
@@ -587,7 +600,39 @@ struct FaKernel {
         // scores are in log2 units of scale * q.k, l = sum 2^(s - m).
         if (!PROBS && a.lse && ks == 0 && hf == 0 && qi < Sq)
             a.lse[(int64_t)bh * Sq + qi] = (m_run + log2f(l_run)) * kLn2;
-        if (ks == 0 && qi < Sq) {
+        if constexpr (O_TRANS) {
+            // O through a per-wave LDS transpose past the merge area: whole
+            // rows of the head (DP floats) per lane group, full lines
+            if (ks == 0) {
+                constexpr int OP = DP + 4;
+                float* const X = reinterpret_cast<float*>(lds_raw + MERGE_BYTES) + qs * QW * OP;
+                const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        *reinterpret_cast<floatx4*>(X + c * OP + db * 32 + 8 * g + 4 * hf) =
+                            floatx4{o[db][4 * g] * linv, o[db][4 * g + 1] * linv, o[db][4 * g + 2] * linv,
+                                    o[db][4 * g + 3] * linv};
+                asm volatile("" ::: "memory");  // other lanes' writes (the wave's LDS accesses are in order)
+                constexpr int LPR = DP / 4;     // lanes per row
+                constexpr int RPI = 64 / LPR;   // rows per instruction
+                const int rr = lane / LPR, cc = 4 * (lane % LPR);
+                float* const o0 = a.o + b * a.o_bs + h * a.o_hs;
+#pragma unroll
+                for (int k = 0; k < QW / RPI; ++k) {
+                    const int row = RPI * k + rr;
+                    const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * OP + cc);
+                    if (qw0 + row < Sq) {
+                        float* dst = o0 + (int64_t)(qw0 + row) * a.o_ts + cc;
+                        if (HIPGPT_O_TRANSPOSE > 1)
+                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
+                        else
+                            *reinterpret_cast<floatx4*>(dst) = v;
+                    }
+                }
+            }
+        } else if (ks == 0 && qi < Sq) {
             const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
 #pragma unroll
