@@ -36,8 +36,14 @@
 namespace hipgpt {
 namespace fa {
 
-// Largest LDS footprint a resident workgroup may use (bytes).
+// Largest LDS footprint of a resident workgroup's tiles (bytes), and of the
+// whole workgroup with the O stores' scratch (the kernel's static LDS, the
+// SIMD ranking, sits in the rest of the 160 KB).
 constexpr int kResidentLdsMax = 152 * 1024;
+constexpr int kResidentLdsLimit = 160 * 1024 - 256;
+#ifndef HIPGPT_RES_O_TRANSPOSE
+#define HIPGPT_RES_O_TRANSPOSE 1
+#endif
 
 #ifndef HIPGPT_RES_SCORES
 #define HIPGPT_RES_SCORES 1
@@ -67,6 +73,12 @@ struct FaResident {
     // The LDS bounds a wave's tiles: ceil(Sk / 32) <= MAX_TILES.
     static constexpr int MAX_TILES = kResidentLdsMax / (TILE_ELEMS * (int)sizeof(E));
     static constexpr int SRES = (HIPGPT_RES_SCORES && PROBS && NKS == 1 && MAX_TILES <= 8) ? MAX_TILES : 0;
+    // O stores through a per-wave 16 x 36 scratch past the tiles (whole
+    // 128-byte row segments, non-temporal): c2 33.9 -> 32.8 us.  Not with
+    // probs, where the larger LDS footprint measured slower (c2 with probs
+    // 41.3 -> 48.6 us, drop-in 56.1 -> 60.3 us).
+    static constexpr bool O_TRANS = HIPGPT_RES_O_TRANSPOSE && !PROBS && sizeof(E) == 4;
+    static constexpr int O_TRANS_BYTES = O_TRANS ? NW * 16 * 36 * 4 : 0;
 
     __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max,
                                                int* simd_slots) {
@@ -373,7 +385,40 @@ struct FaResident {
             }
         }
 
-        if (ks == 0 && qi < Sq) {
+        if constexpr (O_TRANS) {
+            // O through the wave's 16 x 36 scratch past the tiles, one 32-dim
+            // block and 16 query rows at a time: whole 128-byte row segments
+            // per lane group, non-temporal
+            if (ks == 0) {
+                int body = ntiles_max * TILE_ELEMS * (int)sizeof(E);
+                if (body < MERGE_BYTES) body = MERGE_BYTES;
+                float* const X = reinterpret_cast<float*>(lds_raw + HEAD_BYTES + body) + wave * 16 * 36;
+                const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
+                float* const o0 = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qw0 * a.o_ts;
+                const int rr = lane >> 3, cc = 4 * (lane & 7);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        if ((c >> 4) == hh)
+#pragma unroll
+                            for (int g = 0; g < 4; ++g)
+                                *reinterpret_cast<floatx4*>(X + (c - 16 * hh) * 36 + 8 * g + 4 * hf) =
+                                    floatx4{o[db][4 * g] * linv, o[db][4 * g + 1] * linv, o[db][4 * g + 2] * linv,
+                                            o[db][4 * g + 3] * linv};
+                        asm volatile("" ::: "memory");  // other lanes' writes (the wave's LDS accesses are in order)
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const int row = 16 * hh + 8 * k + rr;
+                            const floatx4 v = *reinterpret_cast<const floatx4*>(X + (8 * k + rr) * 36 + cc);
+                            if (qw0 + row < Sq)
+                                __builtin_nontemporal_store(
+                                    v, reinterpret_cast<floatx4*>(o0 + (int64_t)row * a.o_ts + db * 32 + cc));
+                        }
+                        asm volatile("" ::: "memory");  // the next pass's writes come after these reads
+                    }
+            }
+        } else if (ks == 0 && qi < Sq) {
             const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
 #pragma unroll
@@ -403,8 +448,9 @@ inline size_t resident_lds_bytes(const AttnArgs& a) {
     const int64_t tiles = ((int64_t)a.Sk + BK - 1) / BK;
     int64_t body = tiles * R::TILE_ELEMS * (int64_t)sizeof(typename TR::elem);
     if (body < R::MERGE_BYTES) body = R::MERGE_BYTES;
-    const int64_t bytes = R::HEAD_BYTES + body;
-    return (tiles <= 64 && bytes <= kResidentLdsMax) ? (size_t)bytes : 0;
+    using RP = FaResident<TR, NQS, NKS, 4, false, true>;
+    const int64_t bytes = R::HEAD_BYTES + body + (a.probs ? RP::O_TRANS_BYTES : R::O_TRANS_BYTES);
+    return (tiles <= 64 && R::HEAD_BYTES + body <= kResidentLdsMax && bytes <= kResidentLdsLimit) ? (size_t)bytes : 0;
 }
 
 template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
@@ -420,7 +466,7 @@ hipError_t launch_resident_one(const AttnArgs& args, int ntiles, size_t lds, int
     const unsigned long long bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
     if (!bit || !(attr_set.load(std::memory_order_acquire) & bit)) {
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kResidentLdsMax);
+                                kResidentLdsLimit);
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_release);
     }
