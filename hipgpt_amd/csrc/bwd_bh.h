@@ -113,6 +113,33 @@ __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 *
 // the immediate) only, never the scalar offset: a whole tile in range puts
 // each register's row offset in the scalar operand, the last tile of a ragged
 // S (rows past S) folds it into the vector offset so those rows read as zero.
+// A wave's 32 x 32 gradient block (key kj = row0 + c on lane (c, h),
+// register r <-> dim acc_key(r, h)), times mul, stored as whole 128-byte rows
+// through the wave's scratch X (pitch XP), non-temporally; rows past S are
+// dropped.  X must be free: its earlier reads issued (a wave's LDS accesses
+// run in order; the memory clobbers keep the compiler's order).
+#ifndef HIPGPT_BWD_ROWS_T
+#define HIPGPT_BWD_ROWS_T 1
+#endif
+__device__ __forceinline__ void store_rows_t(float* X, float* dst0, const floatx16& acc, float mul, int row0, int S,
+                                             int64_t ts, int lane) {
+    const int c = lane & 31, hf = lane >> 5;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<floatx4*>(X + c * XP + 8 * g + 4 * hf) =
+            floatx4{mul * acc[4 * g], mul * acc[4 * g + 1], mul * acc[4 * g + 2], mul * acc[4 * g + 3]};
+    asm volatile("" ::: "memory");
+    const int rr = lane >> 3, cc = 4 * (lane & 7);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int row = 8 * k + rr;
+        const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * XP + cc);
+        if (row0 + row < S) __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst0 + (int64_t)row * ts + cc));
+    }
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ void load_p_tile(floatx16& pv, __amdgpu_buffer_rsrc_t pr, int i, int kj, bool kval, int hf,
                                             int S) {
     const int S4 = S * 4;
@@ -491,7 +518,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     for (int t = 1; t < nsteps; ++t) job(std::true_type{}, t);
     chain_add(dq_term(), iprev, nsteps - 1);
 
-    if (kval) {
+    if (HIPGPT_BWD_ROWS_T) {
+        // dV, dK through the wave's scratch (its last reads were issued
+        // above): whole 128-byte rows, non-temporal
+        store_rows_t(X, a.dv + base + (int64_t)(kt * BK) * a.ts, accv, 1.f, kt * BK, S, a.ts, lane);
+        store_rows_t(X, a.dk + base + (int64_t)(kt * BK) * a.ts, acck, a.scale, kt * BK, S, a.ts, lane);
+    } else if (kval) {
         float* dvp = a.dv + base + (int64_t)kj * a.ts;
         float* dkp = a.dk + base + (int64_t)kj * a.ts;
 #pragma unroll
@@ -793,7 +825,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
         reduce_dq(Even{}, t);
     }
 
-    if (active && kval) {
+    if (HIPGPT_BWD_ROWS_T && active) {
+        store_rows_t(X, a.dv + base + (int64_t)(wave * BK) * a.ts, accv, 1.f, wave * BK, S, a.ts, lane);
+        store_rows_t(X, a.dk + base + (int64_t)(wave * BK) * a.ts, acck, a.scale, wave * BK, S, a.ts, lane);
+    } else if (active && kval) {
         float* dvp = a.dv + base + (int64_t)kj * a.ts;
         float* dkp = a.dk + base + (int64_t)kj * a.ts;
 #pragma unroll

@@ -418,7 +418,17 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
     if (t < nt) step(Even{}, t, p);
     reduce_dq(nt - 1);
 
-    if (active && kval) {
+    if (HIPGPT_BWD_ROWS_T && active) {
+        // dV, dK through the wave's scratch, one 32-dim block at a time: whole
+        // 128-byte row segments, non-temporal (the scratch's last reads, the
+        // dQ term's operands, were issued before the closing barrier)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            store_rows_t(X, a.dv + base + (int64_t)(wave * BK) * a.ts + 32 * n, accv[n], 1.f, wave * BK, S, a.ts, lane);
+            store_rows_t(X, a.dk + base + (int64_t)(wave * BK) * a.ts + 32 * n, acck[n], a.scale, wave * BK, S, a.ts,
+                         lane);
+        }
+    } else if (active && kval) {
         float* dvp = a.dv + base + (int64_t)kj * a.ts;
         float* dkp = a.dk + base + (int64_t)kj * a.ts;
 #pragma unroll
