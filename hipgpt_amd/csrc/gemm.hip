@@ -61,6 +61,11 @@ struct Cfg {
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
+// Whole-row, non-temporal C stores through LDS (see the epilogue).
+#ifndef HIPGPT_GEMM_ROWS_T
+#define HIPGPT_GEMM_ROWS_T 1
+#endif
+
 template <int BM, int BN, int WM, int WN, int GBK, int NACC, bool VEC, bool BF16OUT>
 __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(GemmArgs g) {
     using C = Cfg<BM, BN, WM, WN, GBK>;
@@ -206,6 +211,49 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         __syncthreads();
     }
 
+    // ---- epilogue, whole-row path: each 32 x 32 block (+ bias) goes through
+    // a per-wave scratch in the (now idle) stage buffers and leaves as whole
+    // 128-byte row segments, non-temporally, when the block is inside C, fp32,
+    // and its 32 columns stay in one segment ----
+    constexpr bool ROWS_T = HIPGPT_GEMM_ROWS_T && VEC && !BF16OUT && C::NW * 32 * 36 <= 2 * C::STAGE;
+    if constexpr (ROWS_T) {
+        float* const X = lds + wave * 32 * 36;
+        const int rr = lane >> 3, cc = 4 * (lane & 7);
+#pragma unroll
+        for (int i = 0; i < C::NB; ++i) {
+            const int nb = n0 + wn0 + 32 * i;  // first column of the block
+#pragma unroll
+            for (int j = 0; j < C::MB; ++j) {
+                const int mb = m0 + wm0 + 32 * j;  // first row of the block
+                const bool whole = mb + 32 <= g.M && nb + 32 <= g.N && nb / g.seg_w == (nb + 31) / g.seg_w;
+                if (!whole) continue;  // left to the general path below
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = nb + 8 * q + 4 * h;
+                    const floatx4 bv = g.bias ? *reinterpret_cast<const floatx4*>(g.bias + n) : zero4();
+                    floatx4 v;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        float t = acc[0][i][j][4 * q + u];
+#pragma unroll
+                        for (int x = 1; x < NACC; ++x) t += acc[x][i][j][4 * q + u];
+                        v[u] = t + bv[u];
+                    }
+                    *reinterpret_cast<floatx4*>(X + c * 36 + 8 * q + 4 * h) = v;
+                }
+                asm volatile("" ::: "memory");  // other lanes' writes (the wave's LDS accesses are in order)
+                float* const cb = static_cast<float*>(g.C) + (int64_t)(nb / g.seg_w) * g.seg_stride + nb % g.seg_w;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int row = 8 * k + rr;
+                    const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
+                    __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(cb + (int64_t)(mb + row) * g.ldc + cc));
+                }
+                asm volatile("" ::: "memory");  // the next block's writes come after these reads
+            }
+        }
+    }
+
     // ---- epilogue: + bias, store (register group q -> columns 8q + 4h .. +3) ----
 #pragma unroll
     for (int i = 0; i < C::NB; ++i) {
@@ -225,6 +273,10 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
             for (int j = 0; j < C::MB; ++j) {
                 const int m = m0 + wm0 + 32 * j + c;
                 if (m >= g.M) continue;
+                if constexpr (ROWS_T) {  // stored above
+                    const int mb = m0 + wm0 + 32 * j, nb = n0 + wn0 + 32 * i;
+                    if (mb + 32 <= g.M && nb + 32 <= g.N && nb / g.seg_w == (nb + 31) / g.seg_w) continue;
+                }
                 floatx4 v;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
