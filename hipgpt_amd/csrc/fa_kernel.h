@@ -108,11 +108,14 @@ struct FaKernel {
     static constexpr bool TRANS_OWN = HIPGPT_PROBS_TRANSPOSE && PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 &&
                                       DP >= HIPGPT_PROBS_TRANSPOSE_MIN_DP;
     static constexpr int LDS_BYTES = BASE_BYTES + (TRANS_OWN ? NW * QW * 36 * 4 : 0);
-    // O stores through LDS (whole rows of the head per lane group) where the
-    // per-wave scratch fits past the merge area within the LDS already used;
-    // only with 16-byte rows of the full padded head (VEC, D = DP).
-    static constexpr bool O_TRANS = HIPGPT_O_TRANSPOSE && VEC && sizeof(E) == 4 && DP <= 64 &&
-                                    MERGE_BYTES + NQS * QW * (DP + 4) * 4 <= BASE_BYTES;
+    // O stores through LDS, one 32-dim block at a time (whole 128-byte row
+    // segments per lane group), with a 32 x 36 scratch per storing wave
+    // (ks == 0) inside the LDS already allocated: past the merge area when it
+    // fits there, else over it after a barrier.  Only with 16-byte rows of the
+    // full padded head (VEC, D = DP).
+    static constexpr int O_SCR = NQS * QW * 36 * 4;
+    static constexpr bool O_TRANS = HIPGPT_O_TRANSPOSE && VEC && O_SCR <= BASE_BYTES;
+    static constexpr bool O_TRANS_PAST = MERGE_BYTES + O_SCR <= BASE_BYTES;
 
     // Global -> register staging of one stage (K and V), 16-byte chunks.
     static constexpr int EPC = 16 / (int)sizeof(E);      // elements per chunk
@@ -601,35 +604,33 @@ struct FaKernel {
         if (!PROBS && a.lse && ks == 0 && hf == 0 && qi < Sq)
             a.lse[(int64_t)bh * Sq + qi] = (m_run + log2f(l_run)) * kLn2;
         if constexpr (O_TRANS) {
-            // O through a per-wave LDS transpose past the merge area: whole
-            // rows of the head (DP floats) per lane group, full lines
+            if constexpr (!O_TRANS_PAST) __syncthreads();  // the merge's reads of the area are done
             if (ks == 0) {
-                constexpr int OP = DP + 4;
-                float* const X = reinterpret_cast<float*>(lds_raw + MERGE_BYTES) + qs * QW * OP;
+                float* const X = reinterpret_cast<float*>(lds_raw + (O_TRANS_PAST ? MERGE_BYTES : 0)) + qs * QW * 36;
                 const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
+                const int rr = lane >> 3, cc = 4 * (lane & 7);
+                float* const o0 = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qw0 * a.o_ts;
 #pragma unroll
-                for (int db = 0; db < NDB; ++db)
+                for (int db = 0; db < NDB; ++db) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
-                        *reinterpret_cast<floatx4*>(X + c * OP + db * 32 + 8 * g + 4 * hf) =
+                        *reinterpret_cast<floatx4*>(X + c * 36 + 8 * g + 4 * hf) =
                             floatx4{o[db][4 * g] * linv, o[db][4 * g + 1] * linv, o[db][4 * g + 2] * linv,
                                     o[db][4 * g + 3] * linv};
-                asm volatile("" ::: "memory");  // other lanes' writes (the wave's LDS accesses are in order)
-                constexpr int LPR = DP / 4;     // lanes per row
-                constexpr int RPI = 64 / LPR;   // rows per instruction
-                const int rr = lane / LPR, cc = 4 * (lane % LPR);
-                float* const o0 = a.o + b * a.o_bs + h * a.o_hs;
+                    asm volatile("" ::: "memory");  // other lanes' writes (the wave's LDS accesses are in order)
 #pragma unroll
-                for (int k = 0; k < QW / RPI; ++k) {
-                    const int row = RPI * k + rr;
-                    const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * OP + cc);
-                    if (qw0 + row < Sq) {
-                        float* dst = o0 + (int64_t)(qw0 + row) * a.o_ts + cc;
-                        if (HIPGPT_O_TRANSPOSE > 1)
-                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
-                        else
-                            *reinterpret_cast<floatx4*>(dst) = v;
+                    for (int k = 0; k < QW / 8; ++k) {
+                        const int row = 8 * k + rr;
+                        const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
+                        if (qw0 + row < Sq) {
+                            float* dst = o0 + (int64_t)row * a.o_ts + db * 32 + cc;
+                            if (HIPGPT_O_TRANSPOSE > 1)
+                                __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
+                            else
+                                *reinterpret_cast<floatx4*>(dst) = v;
+                        }
                     }
+                    asm volatile("" ::: "memory");  // the next block's writes come after these reads
                 }
             }
         } else if (ks == 0 && qi < Sq) {
