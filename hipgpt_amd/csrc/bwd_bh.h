@@ -121,6 +121,11 @@ __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 *
 #ifndef HIPGPT_BWD_ROWS_T
 #define HIPGPT_BWD_ROWS_T 1
 #endif
+// Cache policy of the dQ row stores (whole rows already): 2 = non-temporal.
+#ifndef HIPGPT_DQ_NT
+#define HIPGPT_DQ_NT 1
+#endif
+constexpr int kDqPolicy = HIPGPT_DQ_NT ? 2 : 0;
 __device__ __forceinline__ void store_rows_t(float* X, float* dst0, const floatx16& acc, float mul, int row0, int S,
                                              int64_t ts, int lane) {
     const int c = lane & 31, hf = lane >> 5;
@@ -426,12 +431,12 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr, vo,
-                                                          (8 * (r >> 2) + (r & 3)) * row4, 0);
+                                                          (8 * (r >> 2) + (r & 3)) * row4, kDqPolicy);
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a.scale * aq[r]), dqr,
-                                                          vo + (8 * (r >> 2) + (r & 3)) * row4, 0, 0);
+                                                          vo + (8 * (r >> 2) + (r & 3)) * row4, 0, kDqPolicy);
             }
         } else {
 #pragma unroll
@@ -727,7 +732,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
         }
         typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
         __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a.scale * s0), __float_as_uint(a.scale * s1)}, dqr,
-                                              (i * BK + rrow) * row4 + rd2 * 4, 0, 0);
+                                              (i * BK + rrow) * row4 + rd2 * 4, 0, kDqPolicy);
     };
 
     floatx16 accv, acck;  // dV^T, dK^T (unscaled): register r <-> dim acc_key(r, h), lane <-> key

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
         }
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(a.scale * sm[0]), __float_as_uint(a.scale * sm[1]),
                                                      __float_as_uint(a.scale * sm[2]), __float_as_uint(a.scale * sm[3])},
-                                               dqr, (i * BK + rrow) * row4 + rdd * 4, 0, 0);
+                                               dqr, (i * BK + rrow) * row4 + rdd * 4, 0, kDqPolicy);
     };
 
     lds_barrier();  // ring tile 0, the zeroed slots
