@@ -540,7 +540,7 @@ struct FaKernel {
             // stored before the sweeps, while the first stage's loads are in flight.
             if (CAUSAL && qw0 < Sq && ks == 0) {
                 const bool pv0 = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
-                zero_probs_tail(a.probs + (int64_t)bh * Sq * Sk, qw0, Sq, Sk, tr.wtiles * BK, lane, pv0);
+                zero_probs_tail<(SRT > 0)>(a.probs + (int64_t)bh * Sq * Sk, qw0, Sq, Sk, tr.wtiles * BK, lane, pv0);
             }
 #endif
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
