@@ -66,7 +66,21 @@ __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f};
 #define HIPGPT_GEMM_ROWS_T 1
 #endif
 
-template <int BM, int BN, int WM, int WN, int GBK, int NACC, bool VEC, bool BF16OUT>
+// KF: K is a multiple of GBK (16-byte path only), so no k-tile runs past K:
+// the k offset of the loads rides in the buffer instruction's scalar offset
+// and the per-element k mask goes away.  With the k loop unrolled by two
+// (UNROLL2: each stage buffer at a constant address, the operand reads at
+// loop-invariant bases) the loop issues no VALU work beyond a loop test,
+// which matters because fp32 VALU ops take MFMA issue cycles on gfx950.
+// Cache-rotated, us: c1 QKV 32.6 -> 30.6, c1 out 14.9 -> 13.7, c3 QKV
+// 246 -> 232, c3 out 85.2 -> 80.1 (KF alone: c3 QKV 244, c1 level).
+#ifndef HIPGPT_GEMM_KF
+#define HIPGPT_GEMM_KF 1
+#endif
+#ifndef HIPGPT_GEMM_UNROLL2
+#define HIPGPT_GEMM_UNROLL2 1
+#endif
+template <int BM, int BN, int WM, int WN, int GBK, int NACC, bool VEC, bool BF16OUT, bool KF>
 __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(GemmArgs g) {
     using C = Cfg<BM, BN, WM, WN, GBK>;
     constexpr int APITCH = C::APITCH;
@@ -104,7 +118,11 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
 #pragma unroll
         for (int i = 0; i < C::W_PER; ++i) {
             const int f = tid + i * C::NT;
-            woff[i] = (int)(((f / (BN / 4)) * g.ldw + (f % (BN / 4)) * 4) * 4);
+            const int kr = f / (BN / 4), nc = (f % (BN / 4)) * 4;
+            // KF: columns past N re-read column n0 (in bounds; they only feed
+            // outputs that are never stored), as the scalar k offset is outside
+            // the buffer's range check
+            woff[i] = (int)((kr * g.ldw + (KF && nc >= cols ? 0 : nc)) * 4);
         }
     }
     auto load = [&](int kt) {
@@ -113,7 +131,10 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         for (int i = 0; i < C::A_PER; ++i) {
             const int f = tid + i * C::NT;
             const int r = f / ACPR, kc = (f % ACPR) * 4;
-            if constexpr (VEC) {
+            if constexpr (VEC && KF) {
+                // rows past M read as zero (their voffset is past the range)
+                ar[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff[i], k0 * 4, 0));
+            } else if constexpr (VEC) {
                 // rows past M read as zero (buffer range); k past K is masked
                 // here because it would read the next row's values
                 const floatx4 v = __builtin_bit_cast(
@@ -132,7 +153,10 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         for (int i = 0; i < C::W_PER; ++i) {
             const int f = tid + i * C::NT;
             const int kr = f / (BN / 4), nc = (f % (BN / 4)) * 4;
-            if constexpr (VEC) {
+            if constexpr (VEC && KF) {
+                wr[i] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, woff[i], (int)((int64_t)k0 * g.ldw * 4), 0));
+            } else if constexpr (VEC) {
                 // rows past K read as zero; columns past N only feed outputs
                 // that are never stored
                 wr[i] = __builtin_bit_cast(
@@ -204,12 +228,27 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         store(lds);
     }
     __syncthreads();
+#if HIPGPT_GEMM_UNROLL2
+    // two k-tiles per iteration, so each stage buffer's address is a constant
+    auto step = [&](int kt, auto stage_tag) {
+        constexpr int SB = decltype(stage_tag)::value;
+        if (kt + 1 < nkt) load(kt + 1);
+        compute(lds + SB * C::STAGE);
+        if (kt + 1 < nkt) store(lds + (1 - SB) * C::STAGE);
+        __syncthreads();
+    };
+    for (int kt = 0; kt < nkt; kt += 2) {
+        step(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < nkt) step(kt + 1, std::integral_constant<int, 1>{});
+    }
+#else
     for (int kt = 0; kt < nkt; ++kt) {
         if (kt + 1 < nkt) load(kt + 1);
         compute(lds + (kt & 1) * C::STAGE);
         if (kt + 1 < nkt) store(lds + ((kt + 1) & 1) * C::STAGE);
         __syncthreads();
     }
+#endif
 
     // ---- epilogue, whole-row path: each 32 x 32 block (+ bias) goes through
     // a per-wave scratch in the (now idle) stage buffers and leaves as whole
@@ -318,12 +357,19 @@ hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
     const int64_t tiles = (int64_t)((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     if (tiles <= 0 || tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
     constexpr int NT = Cfg<BM, BN, WM, WN, GBK>::NT;
-    if (g.out_bf16)
-        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, true>), dim3((unsigned)tiles), dim3(NT), 0,
-                           s, g);
-    else
-        hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, false>), dim3((unsigned)tiles), dim3(NT),
-                           0, s, g);
+    const dim3 grid((unsigned)tiles), block(NT);
+    const bool kf = HIPGPT_GEMM_KF && VEC && g.K % GBK == 0;
+    if (g.out_bf16) {
+        if (kf)
+            hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, true, VEC>), grid, block, 0, s, g);
+        else
+            hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, true, false>), grid, block, 0, s, g);
+    } else {
+        if (kf)
+            hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, false, VEC>), grid, block, 0, s, g);
+        else
+            hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, false, false>), grid, block, 0, s, g);
+    }
     return hipGetLastError();
 }
 

@@ -51,9 +51,11 @@ def check_fp32(got, A, B, bias, want):
 
 # (M, N, K) in the reference's naming: A [M, N], B [N, K], C [M, K].
 # Vector path (N, K multiples of 4), ragged edges of both tile shapes, the
-# scalar path (N or K not a multiple of 4), and a tiny problem.
+# scalar path (N or K not a multiple of 4), and a tiny problem.  An inner dim
+# N that is a multiple of 32 takes the whole-k-tile loads; (70, 64, 100) and
+# (129, 96, 260) give them a partial column tile and partial row tiles.
 SHAPES = [(1, 4, 4), (3, 5, 7), (64, 256, 256), (130, 256, 768), (97, 36, 52), (200, 1024, 256),
-          (33, 33, 33), (640, 256, 12), (5, 2, 1000)]
+          (33, 33, 33), (640, 256, 12), (5, 2, 1000), (70, 64, 100), (129, 96, 260)]
 
 
 @pytest.mark.parametrize("with_bias", [True, False])
