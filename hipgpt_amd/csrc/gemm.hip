@@ -377,8 +377,9 @@ hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
 // waves of 32 x 32, k-tiles of 32.  Measured on MI355X against 128x64,
 // 64x64, 128x128, 32x64, 64x32 and 128x64/8-wave tiles, k-tiles of 16 and
 // 64 and two accumulator chains: best or within noise on every projection
-// shape of the c1 and c3 layers (the kernel is latency-bound, so more
-// resident waves beat larger per-wave tiles).
+// shape of the c1 and c3 layers (more resident waves beat larger per-wave
+// tiles).  With the VALU-free k loop, 128x128 (32x64 or 64x32 per wave),
+// 64x128 (32x64 per wave) and 128x64 were again 1-68% slower.
 template <bool VEC>
 hipError_t launch_vec(const GemmArgs& g, hipStream_t s) {
     return launch_cfg<64, 128, 32, 32, VEC>(g, s);
