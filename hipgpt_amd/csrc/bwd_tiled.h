@@ -199,6 +199,7 @@ struct BwdQ {
         kl.init(a.k + base, a.ts, S, a.D);
         vl.init(a.v + base, a.ts, S, a.D);
         floatx4 stg[PER];
+        static_assert((NKS * T::CPT) % 64 == 0, "a wave's chunks are all K or all V");
         auto load = [&](int st) {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -207,7 +208,12 @@ struct BwdQ {
                 const int isk = f >= NKS * T::CPT;
                 const int g = isk ? f - NKS * T::CPT : f;
                 const int row = st * NKS * BK + g / T::CPR;
-                stg[i] = isk ? kl.load(row, g % T::CPR) : vl.load(row, g % T::CPR);
+                // K or V is wave-uniform (NKS * CPT is a multiple of 64): a scalar
+                // branch instead of a per-lane select of two buffer resources
+                if (__builtin_amdgcn_readfirstlane(isk))
+                    stg[i] = kl.load(row, g % T::CPR);
+                else
+                    stg[i] = vl.load(row, g % T::CPR);
             }
         };
         auto store = [&](float* dst) {
@@ -433,6 +439,7 @@ struct BwdKV {
         floatx4 ostg[RECOMP ? NG : 1];  // O chunks matching the dO chunks (recompute mode)
         float dqs = 0.f;   // Dq value this thread stages (stored-probs mode)
         float lses = 0.f;  // lse' value this thread stages (+inf past the last row: P = 0)
+        static_assert((NQS * T::CPT) % 64 == 0, "a wave's chunks are all Q or all dO");
         auto load = [&](int st) {
             const int qt0 = it0 + st * NQS;
 #pragma unroll
@@ -442,7 +449,10 @@ struct BwdKV {
                 const int isq = f >= NQS * T::CPT;
                 const int g = isq ? f - NQS * T::CPT : f;
                 const int row = qt0 * BK + g / T::CPR;
-                stg[i] = isq ? ql.load(row, g % T::CPR) : gl.load(row, g % T::CPR);
+                if (__builtin_amdgcn_readfirstlane(isq))  // wave-uniform, as above
+                    stg[i] = ql.load(row, g % T::CPR);
+                else
+                    stg[i] = gl.load(row, g % T::CPR);
                 if constexpr (RECOMP) {
                     if (i < NG) ostg[i] = ol.load(row, g % T::CPR);
                 }

@@ -62,6 +62,7 @@ struct FaResident {
     static constexpr int CPR = DP / EPC;                 // 16-byte chunks per row
     static constexpr int CPT = BK * CPR;                 // chunks per tile, K (same for V)
     static constexpr int PER = (2 * CPT + NT - 1) / NT;  // K+V chunks per thread per tile
+    static_assert(CPT % 64 == 0, "a wave's chunks are all K or all V");
 
     // LDS layout: [0, 256) arrival counters; [256, 256 + ML_BYTES) per-wave
     // (m, l) for the probs sweep merge; then the tiles.  The final O merge
@@ -146,9 +147,16 @@ struct FaResident {
             constexpr int SL = decltype(slot_tag)::value;
 #pragma unroll
             for (int i = 0; i < PER; ++i)
-                if (act[i])
-                    ring[SL][i] = TR::from_u32x4(isv[i] ? __builtin_amdgcn_raw_buffer_load_b128(vrs, goff[i] + t * vtile, 0, 0)
-                                                        : __builtin_amdgcn_raw_buffer_load_b128(krs, goff[i] + t * ktile, 0, 0));
+                if (act[i]) {
+                    // K or V is wave-uniform (a tile's chunks are a multiple
+                    // of 64): said so, the load takes one scalar resource
+                    // instead of a per-lane select of two, which the compiler
+                    // issues as a loop over the distinct resources.
+                    if (__builtin_amdgcn_readfirstlane(isv[i] ? 1 : 0))
+                        ring[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, goff[i] + t * vtile, 0, 0));
+                    else
+                        ring[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, goff[i] + t * ktile, 0, 0));
+                }
         };
         auto publish = [&](int t, auto slot_tag) {
             constexpr int SL = decltype(slot_tag)::value;
