@@ -379,7 +379,9 @@ hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
 // 64 and two accumulator chains: best or within noise on every projection
 // shape of the c1 and c3 layers (more resident waves beat larger per-wave
 // tiles).  With the VALU-free k loop, 128x128 (32x64 or 64x32 per wave),
-// 64x128 (32x64 per wave) and 128x64 were again 1-68% slower.
+// 64x128 (32x64 per wave) and 128x64 were again 1-68% slower, and so were
+// the four-wave 64x64, 32x128 and 128x32 tiles (1-12%, also on the c1
+// output projection's one-workgroup-per-CU grid).
 template <bool VEC>
 hipError_t launch_vec(const GemmArgs& g, hipStream_t s) {
     return launch_cfg<64, 128, 32, 32, VEC>(g, s);
