@@ -97,6 +97,11 @@ CONFIGS = {
     "gemm_out_c1": (8192, 256, 256, 0, 0, False, "f32", False, "gemm"),
     "gemm_qkv_c3": (8192, 2304, 768, 0, 0, False, "f32", False, "gemm"),
     "gemm_out_c3": (8192, 768, 768, 0, 0, False, "f32", False, "gemm"),
+    # HipGPT's attention block as TransformerLayer::self_attention_forward
+    # issues it (src/transformer_layer.cpp:214-222): QKV projection into the
+    # [T][3E] buffer, the drop-in attention on it (non-causal, probs written),
+    # output projection -- three launches on the null stream per call.
+    "c1_layer": (32, 8, 256, 256, 32, False, "f32", True, "layer"),
 }
 
 
@@ -107,6 +112,12 @@ def work(cfg):
     if kind == "gemm":  # A [M, K] @ W [K, N] + bias: read A, W, bias; write C
         M, N, K = B, H, Sq
         return 2.0 * M * N * K, 4 * (M * K + K * N + N + M * N)
+    if kind == "layer":  # the three calls' work, each counted as its own line counts it
+        T, E = B * Sq, H * D
+        parts = [work((T, 3 * E, E, 0, 0, False, "f32", False, "gemm")),
+                 work((B, H, Sq, Sk, D, causal, dtype, probs, "fwd")),
+                 work((T, E, E, 0, 0, False, "f32", False, "gemm"))]
+        return sum(f for f, _ in parts), sum(b for _, b in parts)
     if kind == "sdp":  # read Q, K; write scores
         return 2.0 * B * Sq * Sk * D, 4 * (2 * B * Sq * D + B * Sq * Sk)
     if kind == "softmax":  # read and write B*S*S (no flops counted)
@@ -151,6 +162,9 @@ def set_bytes(cfg):
     if kind == "gemm":
         M, N, K = B, H, Sq
         return 4 * (M * K + K * N + N + M * N)
+    if kind == "layer":  # x, W_qkv, b_qkv, qkv, attention out, probs, W_out, b_out, y
+        T, E = B * Sq, H * D
+        return 4 * (T * E + E * 3 * E + 3 * E + 3 * T * E + T * E + B * H * Sq * Sk + E * E + E + T * E)
     if kind in ("sdp", "softmax", "wsum"):
         return 4 * (3 * B * Sq * D + 2 * B * Sq * Sk + B * Sq * D)
     E = H * D
@@ -201,6 +215,27 @@ def make_call(cfg, torch, A, dev, seed=SEED):
         c = torch.empty(M, N, device=dev)
         return (lambda: P.launch_matmul_add_bias(a, w, bias, c, M, K, N),
                 {"entry": "launch_matmul_add_bias (null stream)", "M": M, "N": N, "K": K})
+    if kind == "layer":
+        from hipgpt_amd import projection as P
+
+        T, E = B * Sq, H * D
+        x = torch.randn(T, E, device=dev, generator=g)
+        wqkv = torch.randn(E, 3 * E, device=dev, generator=g) * E ** -0.5
+        bqkv = torch.randn(3 * E, device=dev, generator=g)
+        wo = torch.randn(E, E, device=dev, generator=g) * E ** -0.5
+        bo = torch.randn(E, device=dev, generator=g)
+        qkv = torch.empty(T, 3 * E, device=dev)
+        att = torch.empty(T, E, device=dev)
+        p = torch.empty(B, H, Sq, Sk, device=dev)
+        y = torch.empty(T, E, device=dev)
+
+        def layer():
+            P.launch_matmul_add_bias(x, wqkv, bqkv, qkv, T, E, 3 * E)
+            A.launch_multihead_attention(qkv.view(-1), att, p, B, Sq, E, H)
+            P.launch_matmul_add_bias(att, wo, bo, y, T, E, E)
+
+        return layer, {"layer": "[T][3E] QKV buffer, as the reference layer passes it",
+                       "entry": "launch_matmul_add_bias + launch_multihead_attention + launch_matmul_add_bias"}
     if kind in ("sdp", "softmax", "wsum"):
         x = torch.randn(3, B * Sq, D, device=dev, generator=g)
         sc = torch.randn(B * Sq, Sk, device=dev, generator=g)

@@ -55,6 +55,17 @@ def test_backward_and_decode_work_closed_form():
     assert nbytes == 4 * B * H * D * (1 + 2 * kv) + 4 * B * H * D  # q, K, V read; O written
 
 
+def test_layer_work_is_its_three_calls():
+    # QKV projection (T x E @ E x 3E), the drop-in attention (non-causal, probs
+    # written), output projection (T x E @ E x E)
+    B, H, S, D = 32, 8, 256, 32
+    T, E = B * S, H * D
+    flops, nbytes = bench.work(bench.CONFIGS["c1_layer"])
+    assert flops == 2.0 * T * E * 3 * E + 4.0 * B * H * D * S * S + 2.0 * T * E * E
+    assert nbytes == (4 * (T * E + E * 3 * E + 3 * E + T * 3 * E) + 4 * B * H * S * D * 4 + 4 * B * H * S * S
+                      + 4 * (T * E + E * E + E + T * E))
+
+
 @pytest.mark.parametrize("name", list(bench.CONFIGS))
 def test_rotation_covers_the_infinity_cache(name):
     # the sets a config rotates over hold at least 1 GiB together (MI355X's
