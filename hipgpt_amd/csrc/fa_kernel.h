@@ -495,7 +495,12 @@ struct FaKernel {
         float* const mrg = reinterpret_cast<float*>(lds_raw);  // merge scratch (after a barrier)
         float* const m_slot = mrg;                              // [NW][64]
         float* const l_slot = mrg + NW * 64;                    // [NW][64]
-        float* const o_slot = mrg + 2 * NW * 64;                // [NW][16*NDB][64]
+        float* const o_slot = mrg + 2 * NW * 64;                // partial O: [NW][4*NDB][64] float4 (merge
+                                                                // without probs) or [NW][16*NDB][64] (with)
+        // partial O of wave `w`, register group g of block db, as one 16-byte slot per lane
+        auto o_at = [&](int w, int db, int g) {
+            return reinterpret_cast<floatx4*>(o_slot) + ((w * NDB + db) * 4 + g) * 64 + lane;
+        };
 
         if (!PROBS) {
             sweep(std::integral_constant<int, 0>{}, 0.f, nullptr, false);
@@ -508,7 +513,8 @@ struct FaKernel {
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) o_slot[(role * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
+                        for (int g = 0; g < 4; ++g)
+                            *o_at(role, db, g) = floatx4{o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
                 }
                 __syncthreads();
                 if (ks == 0) {
@@ -529,8 +535,11 @@ struct FaKernel {
 #pragma unroll
                         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                o[db][r] = fmaf(o_slot[((role + j) * 16 * NDB + db * 16 + r) * 64 + lane], wj, o[db][r]);
+                            for (int g = 0; g < 4; ++g) {
+                                const floatx4 v = *o_at(role + j, db, g);
+#pragma unroll
+                                for (int u = 0; u < 4; ++u) o[db][4 * g + u] = fmaf(v[u], wj, o[db][4 * g + u]);
+                            }
                     }
                 }
             }
@@ -580,10 +589,12 @@ struct FaKernel {
             }
             if (NKS > 1) {
                 if (ks != 0) {
+                    // (scalar slots here: 16-byte ones spill the D = 64 probs kernel under its 128-register cap)
+                    float* const os = o_slot + role * 16 * NDB * 64;
 #pragma unroll
                     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) o_slot[(role * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
+                        for (int r = 0; r < 16; ++r) os[(db * 16 + r) * 64 + lane] = o[db][r];
                 }
                 __syncthreads();
                 if (ks == 0) {
@@ -592,7 +603,8 @@ struct FaKernel {
 #pragma unroll
                         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) o[db][r] += o_slot[((role + j) * 16 * NDB + db * 16 + r) * 64 + lane];
+                            for (int r = 0; r < 16; ++r)
+                                o[db][r] += o_slot[((role + j) * 16 * NDB + db * 16 + r) * 64 + lane];
                 }
             }
             l_run = 1.0f;
