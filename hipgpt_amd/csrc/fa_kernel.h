@@ -34,7 +34,8 @@ namespace fa {
 // 100 MHz s_memrealtime counter = 350 ns per launch rank, for grids of at
 // most 4 query blocks per (batch, head) that are resident at once and fill
 // at least half of the device's workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
-// measured over 100 .. 800 ns per rank).
+// measured over 100 .. 800 ns per rank; re-measured on cache-rotated inputs
+// at 250 .. 550 ns: within 0.1 us rotated, 350 ns best hot).
 #ifndef HIPGPT_FA_STAGGER_TICKS
 #define HIPGPT_FA_STAGGER_TICKS 35
 #endif
