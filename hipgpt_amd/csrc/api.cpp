@@ -320,10 +320,12 @@ int hipgpt_attn_bwd_qkv_planar(const float* grad_out, const float* qkv, const fl
 int hipgpt_attn_bwd_qkv_planar_noalloc(const float* grad_out, const float* qkv, const float* probs,
                                        float* grad_qkv, int B, int S, int E, int H, int causal,
                                        hipStream_t stream) {
-    if (!grad_out || !qkv || !probs || !grad_qkv || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0)
-        return HIPGPT_ERR_INVALID;
+    // The scratch limit is checked before the pointers, so a problem beyond
+    // it is rejected whatever buffers come with it (nothing is launched).
+    if (B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0) return HIPGPT_ERR_INVALID;
     if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
     if ((uint64_t)B * (uint64_t)H * (uint64_t)S > kScratchFloats) return HIPGPT_ERR_SCRATCH;
+    if (!grad_out || !qkv || !probs || !grad_qkv) return HIPGPT_ERR_INVALID;
     hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, probs, grad_qkv, B, S, E, H, causal ? 1 : 0);
     if (hipgpt::bwd_uses_workspace(a)) {
         a.dvec = scratch_ptr();

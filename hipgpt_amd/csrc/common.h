@@ -81,16 +81,24 @@ __device__ __forceinline__ void note_wait_expired() {
     __hip_atomic_fetch_add(&g_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Host: this translation unit's expiry count on the current device (blocking
-// copy on the null stream), cleared when `clear` is set and it was non-zero.
+// Host: this translation unit's expiry count on the current device.  One
+// thread reads it into g_wait_taken with a device-side atomic (an exchange for
+// zero when `clear` is set, so no expiry between the read and the clear is
+// lost), then a blocking copy on the null stream brings it back.  The count is
+// exact only when no kernel of the library is still running on another stream
+// (the null stream does not wait for non-blocking streams).
+static __device__ unsigned int g_wait_taken;
+
+static __global__ void wait_expired_take_kernel(int clear) {
+    g_wait_taken = clear ? __hip_atomic_exchange(&g_wait_expired, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : __hip_atomic_load(&g_wait_expired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 static inline hipError_t wait_expired_take(unsigned int* count, bool clear) {
-    hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_wait_expired), sizeof(unsigned int), 0,
-                                       hipMemcpyDeviceToHost);
-    if (e == hipSuccess && clear && *count != 0) {
-        const unsigned int zero = 0;
-        e = hipMemcpyToSymbol(HIP_SYMBOL(g_wait_expired), &zero, sizeof(unsigned int), 0, hipMemcpyHostToDevice);
-    }
-    return e;
+    hipLaunchKernelGGL(wait_expired_take_kernel, dim3(1), dim3(1), 0, 0, clear ? 1 : 0);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return hipMemcpyFromSymbol(count, HIP_SYMBOL(g_wait_taken), sizeof(unsigned int), 0, hipMemcpyDeviceToHost);
 }
 
 // Workgroups of kernel `kern` (block threads, dynamic LDS bytes) the current

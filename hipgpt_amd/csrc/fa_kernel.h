@@ -79,8 +79,14 @@ constexpr int kStaggerMaxBlocks = HIPGPT_FA_STAGGER_MAX_BLOCKS;  // 0: no start 
 // SRT < 0 (probs only, rows longer than that): the max/sum sweep stores each
 // masked score tile into the probs buffer, where the probs sweep reads it back
 // and overwrites it with P -- two products instead of three (no second Q K^T,
-// no K staging) for one more write and read of the probs rows.  Each lane
-// reads back only what it wrote, in the same sweep order.
+// no K staging) for one more write and read of the probs rows.  With the
+// accumulator-layout stores each lane reads back only what it wrote, in the
+// same sweep order.  With the per-wave LDS transpose (TRANS_OWN: causal, padded
+// head dim >= 128) a tile's scores leave as whole rows, so lanes write other
+// lanes' rows and the read-back is cross-lane: it is correct only because every
+// sweep iteration ends with a workgroup barrier (and one precedes the first
+// read-back prefetch), which orders each global store before the loads of the
+// other lanes.  A change that removes those barriers breaks the spill.
 template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 struct FaKernel {
     static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");

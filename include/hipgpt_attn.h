@@ -178,7 +178,10 @@ int hipgpt_attn_decode_kvcache(const float* q, const float* k_new,
  * wait that runs out is counted on the device.  *count receives the number
  * of expired waits on the current device since the last clear (zero in a
  * correct run; non-zero means some outputs may be wrong).  clear != 0 resets
- * the count.  Blocking: a copy on the null stream. */
+ * the count in the same device-side atomic that reads it.  Blocking: a
+ * one-thread kernel and a copy on the null stream.  The count is exact only
+ * when no library kernel is in flight on another stream (the null stream does
+ * not wait for non-blocking streams): synchronise the device first. */
 int hipgpt_attn_wait_expired(unsigned int* count, int clear);
 
 /* ---- projections either side of the attention (fp32 MFMA GEMM) ---- */

@@ -58,9 +58,56 @@ def test_noalloc_backward_matches_workspace_entry(dev, first, second, causal):
 
 
 def test_noalloc_backward_rejects_problems_beyond_its_scratch(dev):
+    """B*H*S = 2^21 > 2^20 floats of scratch: rejected on the host before the
+    pointers are looked at, so the call passes null pointers and can never
+    launch anything."""
     L = _lib.lib()
-    x = torch.zeros(16, device=dev)
-    # B*H*S = 2^21 > 2^20 floats of scratch: rejected on the host, nothing launched
-    rc = L.hipgpt_attn_bwd_qkv_planar_noalloc(_ptr(x), _ptr(x), _ptr(x), _ptr(x), 64, 2048, 2048, 16, 0, None)
+    rc = L.hipgpt_attn_bwd_qkv_planar_noalloc(None, None, None, None, 64, 2048, 2048, 16, 0, None)
     assert rc == _lib.ERR_SCRATCH
     assert b"scratch" in L.hipgpt_attn_strerror(rc)
+    # within the limit, the null pointers are what is rejected
+    rc = L.hipgpt_attn_bwd_qkv_planar_noalloc(None, None, None, None, 1, 64, 64, 2, 0, None)
+    assert rc == _lib.ERR_INVALID
+
+
+@pytest.mark.parametrize("B,S,E,H", [(4, 512, 512, 8),    # D = 64: tiled kernels, scratch used
+                                     (2, 300, 512, 4)])   # D = 128: scratch used
+def test_noalloc_backward_under_graph_capture(dev, B, S, E, H):
+    """The noalloc call captured into a HIP graph (after one eager call, which
+    looks up the scratch address and sets kernel attributes): every replay,
+    with eager calls of both entry points in between, equals the caller-
+    workspace entry point bit for bit."""
+    L = _lib.lib()
+    qkv, go, probs = _problem(B, S, E, H, True, 23, dev)
+    ws = torch.empty(L.hipgpt_attn_bwd_workspace_bytes(B, S, H) // 4, device=dev)
+    want = torch.full((3 * B * S * E,), float("nan"), device=dev)
+    got = torch.full_like(want, float("nan"))
+
+    def workspace_call():
+        rc = L.hipgpt_attn_bwd_qkv_planar(_ptr(go), _ptr(qkv), _ptr(probs), _ptr(want), B, S, E, H, 1,
+                                          _ptr(ws), ws.numel() * 4, torch.cuda.current_stream().cuda_stream)
+        assert rc == _lib.OK
+
+    def noalloc_call():
+        rc = L.hipgpt_attn_bwd_qkv_planar_noalloc(_ptr(go), _ptr(qkv), _ptr(probs), _ptr(got), B, S, E, H, 1,
+                                                  torch.cuda.current_stream().cuda_stream)
+        assert rc == _lib.OK
+
+    workspace_call()
+    noalloc_call()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        noalloc_call()
+    torch.cuda.synchronize()
+    for k in range(3):
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {k} differs"
+        workspace_call()
+        noalloc_call()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"eager calls after replay {k} differ"
