@@ -85,6 +85,16 @@ CONFIGS = {
     "c1_bwd_legacy": (32, 8, 256, 256, 32, False, "f32", True, "bwd"),
     "c2_bwd": (32, 8, 256, 256, 64, True, "f32", True, "bwd"),
     "c2_bwd_legacy": (32, 8, 256, 256, 64, False, "f32", True, "bwd"),
+    # ... and at the c3 / c4 shapes (D = 64 and 128, long rows).
+    "c3_bwd": (8, 12, 1024, 1024, 64, True, "f32", True, "bwd"),
+    "c3_bwd_legacy": (8, 12, 1024, 1024, 64, False, "f32", True, "bwd"),
+    "c4_bwd": (4, 16, 2048, 2048, 128, True, "f32", True, "bwd"),
+    "c4_bwd_legacy": (4, 16, 2048, 2048, 128, False, "f32", True, "bwd"),
+    # A head dim above 128 (the reference fallback takes any D = E / H):
+    # forward causal and as the drop-in, and the drop-in backward.
+    "d256": (4, 8, 1024, 1024, 256, True, "f32", False, "fwd"),
+    "d256_legacy": (4, 8, 1024, 1024, 256, False, "f32", True, "fwd"),
+    "d256_bwd_legacy": (4, 8, 1024, 1024, 256, False, "f32", True, "bwd"),
     # The probs-free training pair at the same shapes: forward writing O and the
     # row log-sum-exp, and the backward that recomputes P from it.
     "c1_fwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "fwd_lse"),

@@ -24,6 +24,7 @@
 #include "bwd_bh.h"
 #include "bwd_bh64.h"
 #include "bwd_tiled.h"
+#include "bwd_wide.h"
 #include "common.h"
 #include "fa_common.h"
 #include "kernels.h"
@@ -343,6 +344,15 @@ static bool bh_enough(const BwdArgs& a) {
     return (int64_t)a.B * a.H >= device_cus();
 }
 
+// The head-dim-split kernels of bwd_wide.h: stored probs, D % 4 == 0 up to
+// 256, 16-byte aligned rows.
+static bool bwd_wide_ok(const BwdArgs& a) {
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    return a.probs && a.D % 4 == 0 && a.D <= 256 && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) &&
+           al(a.k) && al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) && al(a.probs) &&
+           ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
+}
+
 bool bwd_uses_workspace(const BwdArgs& a) {
     return a.probs && !(bwd_tiled_ok(a) && bh_enough(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
 }
@@ -356,6 +366,12 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
         if (a.D == 32)
             return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
         return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
+    }
+    if (bwd_wide_ok(a)) {
+        if (a.D <= 32) return bwd::launch_wide<32, 4, 1, 2>(a, s);
+        if (a.D <= 64) return bwd::launch_wide<64, 4, 1, 2>(a, s);
+        if (a.D <= 128) return bwd::launch_wide<128, 4, 2, 2>(a, s);
+        return bwd::launch_wide<256, 2, 4, 1>(a, s);
     }
     if (a.D <= 32) return launch_dp<32>(a, s);
     if (a.D <= 64) return launch_dp<64>(a, s);

@@ -448,46 +448,93 @@ void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
 }
 
 /* ---------------------------------------------------- attention backward */
+typedef struct {
+    const float *grad_out, *qkv, *probs;
+    float *grad_qkv;
+    int B, S, E, H, tid, nthreads;
+} bwd_arg;
+
+/* One (b, h): the kernel's threads (b, i, h) for i = 0..S-1, in order.
+ * Every write lands in head h's columns of batch b's rows, so distinct
+ * (b, h) pairs never touch the same element. */
+static void mha_backward_pair(const bwd_arg *a, int b, int h)
+{
+    const int S = a->S, E = a->E, D = E / a->H;
+    const int64_t plane = (int64_t)a->B * S * E;
+    const float *Q = a->qkv, *K = a->qkv + plane, *V = a->qkv + 2 * plane;
+    float *dQ = a->grad_qkv, *dK = a->grad_qkv + plane, *dV = a->grad_qkv + 2 * plane;
+    const float inv = 1.0f / sqrtf((float)D);
+    for (int i = 0; i < S; ++i) {
+        const int64_t ti = (int64_t)b * S + i;
+        const float *gho = a->grad_out + ti * E + h * D;
+        const float *q = Q + ti * E + h * D;
+        float *dq = dQ + ti * E + h * D;
+        const float *prow = a->probs + (((int64_t)b * a->H + h) * S + i) * S;
+        float ws = 0.0f;
+        for (int j = 0; j < S; ++j) {
+            const float *v = V + ((int64_t)b * S + j) * E + h * D;
+            ws = fmaf(prow[j], dot_fma(gho, v, D), ws);
+        }
+        for (int j = 0; j < S; ++j) {
+            const int64_t tj = (int64_t)b * S + j;
+            const float *k = K + tj * E + h * D;
+            const float *v = V + tj * E + h * D;
+            const float pij = prow[j];
+            const float g = pij * (dot_fma(gho, v, D) - ws);
+            float *dv = dV + tj * E + h * D;
+            float *dk = dK + tj * E + h * D;
+            for (int d = 0; d < D; ++d) {
+                dv[d] += pij * gho[d];
+                dq[d] = fmaf(g * k[d], inv, dq[d]);
+                dk[d] += g * q[d] * inv;
+            }
+        }
+    }
+}
+
+static void *bwd_worker(void *argp)
+{
+    const bwd_arg *a = (const bwd_arg *)argp;
+    for (int idx = a->tid; idx < a->B * a->H; idx += a->nthreads) mha_backward_pair(a, idx / a->H, idx % a->H);
+    return NULL;
+}
+
+int oracle_mha_backward_mt(const float *grad_out, const float *qkv,
+                           const float *probs, float *grad_qkv, int B, int S,
+                           int E, int H, int nthreads)
+{
+    if (B <= 0 || S <= 0 || H <= 0 || E % H != 0) return -1;
+    memset(grad_qkv, 0, (size_t)(3 * (int64_t)B * S * E) * sizeof(float));
+    const int npairs = B * H;
+    if (nthreads <= 0) nthreads = 1;
+    if (nthreads > npairs) nthreads = npairs;
+    bwd_arg *args = (bwd_arg *)calloc((size_t)nthreads, sizeof(bwd_arg));
+    pthread_t *th = (pthread_t *)calloc((size_t)nthreads, sizeof(pthread_t));
+    if (!args || !th) {
+        free(args);
+        free(th);
+        return -2;
+    }
+    for (int t = 0; t < nthreads; ++t) args[t] = (bwd_arg){grad_out, qkv, probs, grad_qkv, B, S, E, H, t, nthreads};
+    int started = 1;
+    for (int t = 1; t < nthreads; ++t) {
+        if (pthread_create(&th[t], NULL, bwd_worker, &args[t]) != 0) break;
+        ++started;
+    }
+    bwd_worker(&args[0]);
+    for (int t = 1; t < started; ++t) pthread_join(th[t], NULL);
+    /* pairs of threads that could not start, on this thread */
+    for (int t = started; t < nthreads; ++t) bwd_worker(&args[t]);
+    free(args);
+    free(th);
+    return 0;
+}
+
 int oracle_mha_backward(const float *grad_out, const float *qkv,
                         const float *probs, float *grad_qkv, int B, int S,
                         int E, int H)
 {
-    if (B <= 0 || S <= 0 || H <= 0 || E % H != 0) return -1;
-    const int D = E / H;
-    const int64_t plane = (int64_t)B * S * E;
-    const float *Q = qkv, *K = qkv + plane, *V = qkv + 2 * plane;
-    float *dQ = grad_qkv, *dK = grad_qkv + plane, *dV = grad_qkv + 2 * plane;
-    memset(grad_qkv, 0, (size_t)(3 * plane) * sizeof(float));
-    const float inv = 1.0f / sqrtf((float)D);
-    for (int b = 0; b < B; ++b)
-        for (int h = 0; h < H; ++h)
-            for (int i = 0; i < S; ++i) {
-                const int64_t ti = (int64_t)b * S + i;
-                const float *gho = grad_out + ti * E + h * D;
-                const float *q = Q + ti * E + h * D;
-                float *dq = dQ + ti * E + h * D;
-                const float *prow = probs + (((int64_t)b * H + h) * S + i) * S;
-                float ws = 0.0f;
-                for (int j = 0; j < S; ++j) {
-                    const float *v = V + ((int64_t)b * S + j) * E + h * D;
-                    ws = fmaf(prow[j], dot_fma(gho, v, D), ws);
-                }
-                for (int j = 0; j < S; ++j) {
-                    const int64_t tj = (int64_t)b * S + j;
-                    const float *k = K + tj * E + h * D;
-                    const float *v = V + tj * E + h * D;
-                    const float pij = prow[j];
-                    const float g = pij * (dot_fma(gho, v, D) - ws);
-                    float *dv = dV + tj * E + h * D;
-                    float *dk = dK + tj * E + h * D;
-                    for (int d = 0; d < D; ++d) {
-                        dv[d] += pij * gho[d];
-                        dq[d] = fmaf(g * k[d], inv, dq[d]);
-                        dk[d] += g * q[d] * inv;
-                    }
-                }
-            }
-    return 0;
+    return oracle_mha_backward_mt(grad_out, qkv, probs, grad_qkv, B, S, E, H, 1);
 }
 
 /* ------------------------------------------------------------------ GEMM */

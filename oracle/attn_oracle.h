@@ -121,6 +121,11 @@ void oracle_attention_weighted_sum(const float *P, const float *V, float *out,
 int oracle_mha_backward(const float *grad_out, const float *qkv,
                         const float *probs, float *grad_qkv, int B, int S,
                         int E, int H);
+/* The same on `nthreads` host threads, (b, h) pairs dealt round-robin:
+ * distinct pairs write disjoint elements, so the result is identical. */
+int oracle_mha_backward_mt(const float *grad_out, const float *qkv,
+                           const float *probs, float *grad_qkv, int B, int S,
+                           int E, int H, int nthreads);
 
 /* Restatement of matmul_add_bias_tiled_kernel (src/hip_kernels.cpp:113-143;
  * bias == NULL: matmul_tiled_kernel, :70-100): A [M][N], B [N][K], C [M][K]

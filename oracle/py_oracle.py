@@ -67,6 +67,8 @@ def _oracle():
         L.oracle_softmax_rows.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int] * 3
         L.oracle_mha_backward.restype = ctypes.c_int
         L.oracle_mha_backward.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 4
+        L.oracle_mha_backward_mt.restype = ctypes.c_int
+        L.oracle_mha_backward_mt.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5
         L.oracle_matmul_add_bias.restype = ctypes.c_int
         L.oracle_matmul_add_bias.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3
         L.oracle_launch_multihead_attention.restype = ctypes.c_int
@@ -187,14 +189,21 @@ def attention_weighted_sum(P, V, B, S, D, nthreads=None):
     return out
 
 
-def mha_backward(grad_out, qkv, probs, B, S, E, H):
+def mha_backward(grad_out, qkv, probs, B, S, E, H, nthreads=None):
     """Restatement of launch_multihead_attention_backward
-    (src/hip_kernels.cpp:1159-1272); returns grad_qkv [3*B*S*E]."""
+    (src/hip_kernels.cpp:1159-1272); returns grad_qkv [3*B*S*E].  nthreads
+    > 1 spreads the (b, h) pairs over host threads (same result)."""
     g = np.ascontiguousarray(grad_out, dtype=np.float32)
     x = np.ascontiguousarray(qkv, dtype=np.float32)
     p = np.ascontiguousarray(probs, dtype=np.float32)
     out = np.zeros(3 * B * S * E, dtype=np.float32)
-    if _oracle().oracle_mha_backward(g.ctypes.data, x.ctypes.data, p.ctypes.data, out.ctypes.data, B, S, E, H) != 0:
+    L = _oracle()
+    if nthreads is None or nthreads <= 1:
+        rc = L.oracle_mha_backward(g.ctypes.data, x.ctypes.data, p.ctypes.data, out.ctypes.data, B, S, E, H)
+    else:
+        rc = L.oracle_mha_backward_mt(g.ctypes.data, x.ctypes.data, p.ctypes.data, out.ctypes.data, B, S, E, H,
+                                      nthreads)
+    if rc != 0:
         raise ValueError(f"Bad MHA config: E={E} H={H}")
     return out
 

@@ -221,3 +221,16 @@ def test_backward_restatement_matches_finite_differences(B, S, E, H, causal):
     assert np.abs(got - num).max() < 2e-5 * max(1.0, np.abs(num).max())
     with pytest.raises(ValueError, match="Bad MHA config"):
         O.mha_backward(go, qkv, p64.astype(np.float32), B, S, E, 0)
+
+
+def test_backward_restatement_threads_give_identical_results():
+    """oracle_mha_backward_mt: (b, h) pairs on several host threads write
+    disjoint elements, so the result equals the one-thread restatement bit
+    for bit."""
+    B, S, E, H = 3, 37, 96, 4
+    qkv = O.seeded_planar(77, B, S, E)
+    go = O.fill_normal(78, B * S * E)
+    _, p = O.launch_multihead_attention(qkv, B, S, E, H, causal=True, want_probs=True)
+    one = O.mha_backward(go, qkv, p, B, S, E, H)
+    for nt in (2, 5, 64):
+        assert np.array_equal(O.mha_backward(go, qkv, p, B, S, E, H, nthreads=nt), one)
