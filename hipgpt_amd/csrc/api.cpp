@@ -46,13 +46,18 @@ int attn_dispatch(const AttnArgs& in, int causal, int dtype, hipStream_t stream)
         return from_hip(hipgpt::launch_fa_bf16(a, causal != 0, stream));
     }
 
+    // 16-byte rows: aligned bases and strides, K / V slices within 2^31 bytes
+    const bool rows16 = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+                        a.q_bs % 4 == 0 && a.q_ts % 4 == 0 && a.q_hs % 4 == 0 && a.k_bs % 4 == 0 &&
+                        a.k_ts % 4 == 0 && a.k_hs % 4 == 0 && a.v_bs % 4 == 0 && a.v_ts % 4 == 0 &&
+                        a.v_hs % 4 == 0 && a.o_bs % 4 == 0 && a.o_ts % 4 == 0 && a.o_hs % 4 == 0 &&
+                        kv_slice_fits_32bit(a, 4);
     const int dp = hipgpt::fa_f32_padded_dim(a.D);
-    if (dp == 0) return from_hip(hipgpt::launch_attn_generic_f32(a, causal != 0, stream));
-    const bool vec = a.D == dp && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
-                     (!a.probs || aligned16(a.probs)) && a.q_bs % 4 == 0 && a.q_ts % 4 == 0 &&
-                     a.q_hs % 4 == 0 && a.k_bs % 4 == 0 && a.k_ts % 4 == 0 && a.k_hs % 4 == 0 &&
-                     a.v_bs % 4 == 0 && a.v_ts % 4 == 0 && a.v_hs % 4 == 0 && a.o_bs % 4 == 0 &&
-                     a.o_ts % 4 == 0 && a.o_hs % 4 == 0 && kv_slice_fits_32bit(a, 4);
+    if (dp == 0) {
+        if (hipgpt::fa_wide_supported(a.D) && rows16) return from_hip(hipgpt::launch_fa_wide(a, causal != 0, stream));
+        return from_hip(hipgpt::launch_attn_generic_f32(a, causal != 0, stream));
+    }
+    const bool vec = a.D == dp && rows16 && (!a.probs || aligned16(a.probs));
     return from_hip(hipgpt::launch_fa_f32(a, causal != 0, vec, stream));
 }
 

@@ -100,22 +100,6 @@ struct Tiles {
     }
 };
 
-// 16-byte chunks of `rows` consecutive rows (row stride ts floats) through a
-// buffer resource whose range ends at the slice's last row: rows past it read
-// as zero.
-struct RowLoader {
-    __amdgpu_buffer_rsrc_t rs;
-    int row_bytes;
-    __device__ __forceinline__ void init(const float* base, int64_t ts, int S, int D) {
-        rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)(((int64_t)(S - 1) * ts + D) * 4),
-                                               kBufferFlags);
-        row_bytes = (int)(ts * 4);
-    }
-    __device__ __forceinline__ floatx4 load(int row, int col4) const {
-        return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, row * row_bytes + col4 * 16, 0, 0));
-    }
-};
-
 // Wave role from its SIMD rank sr and the workgroup's launch rank.  The
 // launch ranks of one (b, h) are dealt to the same CUs in turn, so a CU holds
 // one workgroup of each rank.  Rotating the roles by the rank spreads causal

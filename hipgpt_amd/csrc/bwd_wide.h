@@ -22,139 +22,17 @@
 // the diagonal) skips tiles the same way bwd_tiled.h does.
 #pragma once
 
-#include "bwd_tiled.h"
 #include "common.h"
 #include "fa_common.h"
 #include "kernels.h"
+#include "rowtiles.h"
 
 namespace hipgpt {
 namespace bwd {
 
-template <int DP, int DH>
-struct WTiles {
-    static constexpr int RP = DP + 4;     // row pitch (floats)
-    static constexpr int ROW = BK * RP;   // floats of a row-major tile
-    static constexpr int CPR = DP / 4;    // 16-byte chunks per row
-    static constexpr int CPT = BK * CPR;  // chunks per tile
-    static constexpr int DW = DP / DH;    // head dims per wave
-    static constexpr int NDBW = DW / 32;  // 32-dim blocks per wave
-    static_assert(DW % 32 == 0, "a wave holds whole 32-dim blocks");
-
-    // acc[m = row c of rt][n = c] += sum over the wave's dims d of rt[c][d] b[d],
-    // lane (c, h) taking d = dh*DW + h*DW/2 + s (b holds the lane's DW/2 values).
-    __device__ __forceinline__ static void dchain(floatx16& acc, const float* rt, const float* b, int c, int hf,
-                                                  int dh) {
-        const float* rr = rt + c * RP + dh * DW + hf * (DW / 2);
-#pragma unroll
-        for (int j = 0; j < DW / 8; ++j) {
-            const floatx4 kv = *reinterpret_cast<const floatx4*>(rr + 4 * j);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[u], b[4 * j + u], acc, 0, 0, 0);
-        }
-    }
-    // acc[n][db][m = d][n = c] += sum_k rm[k][d] x[n][k][c] over the 32 tile
-    // rows k, for the wave's dim blocks (d = dh*DW + db*32 + c); x in
-    // accumulator register order (register 4g + u <-> row 8g + 4h + u).
-    template <int N>
-    __device__ __forceinline__ static void rchain(floatx16 (*acc)[NDBW], const float* rm, const floatx16* x, int c,
-                                                  int hf, int dh) {
-#pragma unroll
-        for (int db = 0; db < NDBW; ++db) {
-            const float* p = rm + 4 * hf * RP + dh * DW + db * 32 + c;
-            float av[16];
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) av[4 * g + u] = p[(8 * g + u) * RP];
-#pragma unroll
-            for (int t = 0; t < 16; ++t)
-#pragma unroll
-                for (int n = 0; n < N; ++n)
-                    acc[n][db] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[t], x[n][t], acc[n][db], 0, 0, 0);
-        }
-    }
-    // Sum of the DH partial dP tiles of sub-block sb, in wave order (every
-    // wave of the sub-block gets the same bits).  xch: [NW][4][64] floatx4.
-    // The caller has stored its own partial and passed a barrier.
-    __device__ __forceinline__ static floatx16 total(const floatx16& mine, const floatx4* xch, int sb, int dh,
-                                                     int lane) {
-        floatx16 t;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) t[r] = 0.f;
-#pragma unroll
-        for (int j = 0; j < DH; ++j) {
-            floatx16 p;
-            if (j == dh) {
-                p = mine;
-            } else {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const floatx4 v = xch[((sb * DH + j) * 4 + g) * 64 + lane];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) p[4 * g + u] = v[u];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) t[r] += p[r];
-        }
-        return t;
-    }
-    __device__ __forceinline__ static void publish(const floatx16& mine, floatx4* xch, int wave, int lane) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-            xch[(wave * 4 + g) * 64 + lane] = floatx4{mine[4 * g], mine[4 * g + 1], mine[4 * g + 2], mine[4 * g + 3]};
-    }
-    // This lane's DW/2 values of row `row` (dims dh*DW + h*DW/2 ..), zero past
-    // D or past the last row.
-    __device__ __forceinline__ static void load_lane_row(float* dst, const float* x, int row, int S, int D, int64_t ts,
-                                                         int dh, int hf) {
-        const int d0 = dh * DW + hf * (DW / 2);
-        const float* p = x + (int64_t)row * ts + d0;
-#pragma unroll
-        for (int s = 0; s < DW / 2; s += 4) {
-            const floatx4 t = (row < S && d0 + s < D) ? *reinterpret_cast<const floatx4*>(p + s)
-                                                      : floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[s + j] = t[j];
-        }
-    }
-};
-
-// Stage loads shared by both kernels: two row-major tiles of 32 rows (tile 0
-// from loader l0, tile 1 from l1), 16-byte chunks spread over the workgroup,
-// chunks at or past D read as zero.
-template <int DP, int NT>
-struct WStage {
-    static constexpr int CPR = DP / 4;
-    static constexpr int CPT = BK * CPR;
-    static constexpr int PER = (2 * CPT + NT - 1) / NT;
-    static_assert(CPT % 64 == 0, "a wave's chunks all come from one tile");
-    floatx4 v[PER];
-
-    __device__ __forceinline__ void load(const RowLoader& l0, const RowLoader& l1, int row0, int D, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int f = tid + i * NT;
-            if ((2 * CPT) % NT != 0 && f >= 2 * CPT) break;
-            const int second = f >= CPT;
-            const int g = second ? f - CPT : f;
-            const int row = row0 + g / CPR, cc = g % CPR;
-            floatx4 t = __builtin_amdgcn_readfirstlane(second) ? l1.load(row, cc) : l0.load(row, cc);
-            if (cc * 4 >= D) t = floatx4{0.f, 0.f, 0.f, 0.f};
-            v[i] = t;
-        }
-    }
-    __device__ __forceinline__ void store(float* dst, int rp, int tile_floats, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int f = tid + i * NT;
-            if ((2 * CPT) % NT != 0 && f >= 2 * CPT) break;
-            const int second = f >= CPT;
-            const int g = second ? f - CPT : f;
-            *reinterpret_cast<floatx4*>(dst + second * tile_floats + (g / CPR) * rp + (g % CPR) * 4) = v[i];
-        }
-    }
-};
+using fa::acc_key;
+using fa::BK;
+using fa::halves_sum;
 
 // ----------------------------------------------------------------- dQ, Dq
 // Workgroup: NQB query sub-blocks x DH dim slices; NBUF stage buffers (2:
@@ -162,7 +40,7 @@ struct WStage {
 // registers and is stored after a barrier).
 template <int DP, int NQB, int DH, int NBUF, bool CAUSAL>
 struct WideQ {
-    using T = WTiles<DP, DH>;
+    using T = RowTiles<DP, DH>;
     static constexpr int NW = NQB * DH;
     static constexpr int NT = NW * 64;
     static constexpr int STAGE = 2 * T::ROW;  // V, K (row-major)
@@ -188,7 +66,7 @@ struct WideQ {
         RowLoader vl, kl;
         vl.init(a.v + base, a.ts, S, D);
         kl.init(a.k + base, a.ts, S, D);
-        WStage<DP, NT> stg;
+        RowStage<DP, NT, 2> stg;
         floatx4* const xch = reinterpret_cast<floatx4*>(lds + NBUF * STAGE);
 
         floatx16 acc[2][T::NDBW];  // A^T, Bm^T: [d][query]
@@ -219,7 +97,7 @@ struct WideQ {
 
         if (nstages > 0) {
             stg.load(vl, kl, 0, D, tid);
-            stg.store(lds, T::RP, T::ROW, tid);
+            stg.store(lds, T::ROW, tid);
         }
         __syncthreads();
         for (int st = 0; st < nstages; ++st) {
@@ -252,12 +130,12 @@ struct WideQ {
                 T::template rchain<2>(acc, cur + T::ROW, x, c, hf, dh);  // A^T += K^T (P o dP)^T, Bm^T += K^T P^T
             }
             if constexpr (NBUF == 2) {
-                if (st + 1 < nstages) stg.store(lds + ((st + 1) & 1) * STAGE, T::RP, T::ROW, tid);
+                if (st + 1 < nstages) stg.store(lds + ((st + 1) & 1) * STAGE, T::ROW, tid);
                 __syncthreads();
             } else {
                 __syncthreads();
                 if (st + 1 < nstages) {
-                    stg.store(lds, T::RP, T::ROW, tid);
+                    stg.store(lds, T::ROW, tid);
                     __syncthreads();
                 }
             }
@@ -286,7 +164,7 @@ struct WideQ {
 // ----------------------------------------------------------------- dK, dV
 template <int DP, int NKB, int DH, int NBUF, bool CAUSAL>
 struct WideKV {
-    using T = WTiles<DP, DH>;
+    using T = RowTiles<DP, DH>;
     static constexpr int NW = NKB * DH;
     static constexpr int NT = NW * 64;
     static constexpr int DQ_OFF = 2 * T::ROW;
@@ -315,7 +193,7 @@ struct WideKV {
         RowLoader gl, ql;
         gl.init(a.go + base, a.ts, S, D);
         ql.init(a.q + base, a.ts, S, D);
-        WStage<DP, NT> stg;
+        RowStage<DP, NT, 2> stg;
         float dqs = 0.f;
         floatx4* const xch = reinterpret_cast<floatx4*>(lds + NBUF * STAGE);
 
@@ -341,7 +219,7 @@ struct WideKV {
             if (tid < BK) dqs = row0 + tid < S ? a.dvec[(int64_t)bh * S + row0 + tid] : 0.f;
         };
         auto store = [&](float* dst) {
-            stg.store(dst, T::RP, T::ROW, tid);
+            stg.store(dst, T::ROW, tid);
             if (tid < BK) dst[DQ_OFF + tid] = dqs;
         };
         floatx16 pnext;

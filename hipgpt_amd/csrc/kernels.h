@@ -18,7 +18,12 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
 bool fa_bf16_supported(int D);
 hipError_t launch_fa_bf16(const AttnArgs& a, bool causal, hipStream_t stream);
 
-// Any head dim, fp32: one wave per query row (the path for D > 128).
+// fp32 MFMA attention for 128 < D <= 256 with D % 4 == 0 (head dim split over
+// four waves per query sub-block); needs 16-byte aligned rows.
+bool fa_wide_supported(int D);
+hipError_t launch_fa_wide(const AttnArgs& a, bool causal, hipStream_t stream);
+
+// Any head dim, fp32: one wave per query row (the path for other D > 128).
 hipError_t launch_attn_generic_f32(const AttnArgs& a, bool causal, hipStream_t stream);
 
 // Expired bounded waits (note_wait_expired) of the kernels in fa_f32.hip (the

@@ -316,3 +316,55 @@ def test_unfused_helpers_unaligned_views(dev):
     assert np.abs(host(probs).reshape(B * S, S) - wp).max() <= TOL_P
     wo = O.attention_weighted_sum(host(probs).reshape(B * S, S), x[2], B, S, D)
     assert np.abs(host(out).reshape(B * S, D) - wo).max() <= TOL_O
+
+
+# Head dims above 128 with D % 4 == 0 run the head-dim-split MFMA kernel
+# (fa_wide.hip; four waves per 32 queries, 64 dims each, padded to 256); other
+# D above 128 the one-wave-per-row kernel (generic.hip).  S below, across and
+# off the 32-row tile, several query blocks per (b, h), Sq < Sk.
+WIDE_FWD = [
+    (2, 33, 33, 2, 132), (1, 1, 1, 2, 256), (1, 70, 70, 3, 160), (2, 130, 130, 2, 192), (1, 257, 257, 1, 256),
+    (1, 100, 100, 2, 200), (2, 40, 90, 2, 256), (1, 300, 300, 1, 228), (1, 64, 64, 2, 150), (1, 9, 40, 2, 260),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,Sq,Sk,H,D", WIDE_FWD)
+def test_wide_head_dim_forward_matches_oracle(dev, B, Sq, Sk, H, D, causal):
+    """[B, S, H, D] views with probs (NaN directly after the probs in the same
+    allocation: a store past the last row would be visible as a changed
+    value; every probability written) and without, against the oracle."""
+    q, k, v = O.seeded_bshd(D * 31 + Sq + Sk, B, Sq, Sk, H, D)
+    want_o, want_p = O.attention(q, k, v, causal=causal, want_probs=True)
+    dq, dk, dv = dev_t(q), dev_t(k), dev_t(v)
+    n = B * H * Sq * Sk
+    pbuf = torch.full((n + 4096,), float("nan"), device=dev)
+    probs = pbuf[:n].view(B, H, Sq, Sk)
+    out = A.attention(dq, dk, dv, probs=probs, causal=causal)
+    got_p = host(pbuf)
+    assert np.isnan(got_p[n:]).all()
+    assert np.isfinite(got_p[:n]).all()
+    assert np.abs(host(out) - want_o).max() <= TOL_O
+    assert np.abs(got_p[:n].reshape(B, H, Sq, Sk) - want_p).max() <= TOL_P
+    out2 = A.attention(dq, dk, dv, causal=causal)
+    assert np.abs(host(out2) - want_o).max() <= TOL_O
+
+
+@pytest.mark.parametrize("B,S,E,H", [(2, 130, 512, 2), (1, 300, 640, 4), (1, 77, 1024, 4)])
+def test_wide_head_dim_dropin_matches_reference_launcher(dev, B, S, E, H):
+    """HipGPT's call at D = 256, 160, 256: against the reference's launcher
+    (its fallback kernel) on the same device buffers, with and without probs."""
+    ref = _ref_or_skip()
+    qkv = O.seeded_planar(171 + S + E, B, S, E)
+    d_qkv = dev_t(qkv)
+    r_out = torch.zeros((B * S, E), device=dev)
+    r_p = torch.zeros((B, H, S, S), device=dev)
+    ref.launch(d_qkv.data_ptr(), r_out.data_ptr(), r_p.data_ptr(), B, S, E, H)
+    o_out = torch.full((B * S, E), float("nan"), device=dev)
+    o_p = torch.full((B, H, S, S), float("nan"), device=dev)
+    A.launch_multihead_attention(d_qkv, o_out, o_p, B, S, E, H)
+    assert np.abs(host(o_out) - host(r_out)).max() <= TOL_O
+    assert np.abs(host(o_p) - host(r_p)).max() <= TOL_P
+    o2 = torch.full((B * S, E), float("nan"), device=dev)
+    A.launch_multihead_attention(d_qkv, o2, None, B, S, E, H)
+    assert np.abs(host(o2) - host(r_out)).max() <= TOL_O
