@@ -100,6 +100,8 @@ CONFIGS = {
     "c1_fwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "fwd_lse"),
     "c1_bwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "bwd_lse"),
     "c2_bwd_lse": (32, 8, 256, 256, 64, True, "f32", False, "bwd_lse"),
+    "c4_fwd_lse": (4, 16, 2048, 2048, 128, True, "f32", False, "fwd_lse"),
+    "c4_bwd_lse": (4, 16, 2048, 2048, 128, True, "f32", False, "bwd_lse"),
     # The projections either side of the attention (launch_matmul_add_bias,
     # src/transformer_layer.cpp:217, :220) as (M, N, K, -, -, ...): the c1
     # layer (T = 8192 tokens, E = 256) and the GPT-2-small c3 layer (E = 768).
@@ -281,7 +283,8 @@ def make_call(cfg, torch, A, dev, seed=SEED):
                     {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_fwd_lse_qkv_planar"})
         go = torch.randn(B * Sq * E, device=dev, generator=g)
         grad = torch.empty(3 * B * Sq * E, device=dev)
-        return (lambda: A.bwd_lse_qkv_planar(go, qkv, out, lse, grad, B, Sq, E, H, causal=causal),
+        ws = None if D in (32, 64) else torch.empty(B * H * Sq, device=dev)  # row dots dO . O
+        return (lambda: A.bwd_lse_qkv_planar(go, qkv, out, lse, grad, B, Sq, E, H, causal=causal, workspace=ws),
                 {"layout": "planar [3][B*S][E]", "entry": "hipgpt_attn_bwd_lse_qkv_planar"})
     if dtype == "f32" and Sq == Sk:
         # the reference's planar [Q|K|V] buffer

@@ -175,10 +175,15 @@ def bwd_lse_qkv_planar(grad_out, qkv, out, lse, grad_qkv, B, S, E, H, causal=Fal
                        ("grad_qkv", grad_qkv, 3 * n)):
         _need_cuda(name, t, torch.float32)
         _need_numel(name, t, k)
-    del workspace  # accepted for symmetry with attention_backward; this pair needs none
+    # head dims other than 32 / 64 pass the row dots dO . O between their two
+    # kernels through a B*H*S workspace
+    if workspace is None and E // H not in (32, 64):
+        need = int(_lib.lib().hipgpt_attn_bwd_workspace_bytes(B, S, H))
+        workspace = torch.empty(max(1, need // 4), device=qkv.device, dtype=torch.float32)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = _lib.lib().hipgpt_attn_bwd_lse_qkv_planar(
         _ptr(grad_out), _ptr(qkv), _ptr(out), _ptr(lse), _ptr(grad_qkv), B, S, E, H, int(bool(causal)),
-        None, 0, _stream(stream))
+        _ptr(workspace), ws_bytes, _stream(stream))
     _lib.check(rc, "hipgpt_attn_bwd_lse_qkv_planar")
     return grad_qkv
 

@@ -343,8 +343,7 @@ int hipgpt_attn_fwd_lse_qkv_planar(const float* d_qkv, float* d_output, float* l
                                    int causal, hipStream_t stream) {
     if (!d_qkv || !d_output || !lse || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0) return HIPGPT_ERR_INVALID;
     const int D = E / H;
-    if ((D != 32 && D != 64) || E % 4 != 0 || !aligned16(d_qkv) || !aligned16(d_output))
-        return HIPGPT_ERR_UNSUPPORTED;
+    if (D % 4 != 0 || D > 256 || !aligned16(d_qkv) || !aligned16(d_output)) return HIPGPT_ERR_UNSUPPORTED;
     AttnArgs a = planar_args(d_qkv, d_output, nullptr, B, S, E, H);
     a.lse = lse;
     return attn_dispatch(a, causal, HIPGPT_F32, stream);
@@ -356,12 +355,16 @@ int hipgpt_attn_bwd_lse_qkv_planar(const float* grad_out, const float* qkv, cons
     if (!grad_out || !qkv || !out || !lse || !grad_qkv || B <= 0 || S <= 0 || E <= 0 || H <= 0 || E % H != 0)
         return HIPGPT_ERR_INVALID;
     if ((int64_t)B * H > 0x7fffffff) return HIPGPT_ERR_INVALID;
-    (void)workspace;  // not needed: the row dots dO . O are formed in the kernels
-    (void)workspace_bytes;
     hipgpt::BwdArgs a = planar_bwd_args(grad_out, qkv, nullptr, grad_qkv, B, S, E, H, causal ? 1 : 0);
     a.o = out;
     a.lse = lse;
-    if (!hipgpt::bwd_tiled_ok(a)) return HIPGPT_ERR_UNSUPPORTED;
+    if (!hipgpt::bwd_recompute_ok(a)) return HIPGPT_ERR_UNSUPPORTED;
+    // D = 32 / 64 form the row dots dO . O inside each kernel; the other head
+    // dims pass them from the first kernel to the second through the workspace
+    if (hipgpt::bwd_uses_workspace(a)) {
+        if (!workspace || workspace_bytes < hipgpt_attn_bwd_workspace_bytes(B, S, H)) return HIPGPT_ERR_WORKSPACE;
+        a.dvec = static_cast<float*>(workspace);
+    }
     return from_hip(hipgpt::launch_attn_bwd(a, stream));
 }
 

@@ -344,22 +344,26 @@ static bool bh_enough(const BwdArgs& a) {
     return (int64_t)a.B * a.H >= device_cus();
 }
 
-// The head-dim-split kernels of bwd_wide.h: stored probs, D % 4 == 0 up to
-// 256, 16-byte aligned rows.
+// The head-dim-split kernels of bwd_wide.h: D % 4 == 0 up to 256, 16-byte
+// aligned rows; stored probs, or recompute mode from O and lse.
 static bool bwd_wide_ok(const BwdArgs& a) {
     auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    return a.probs && a.D % 4 == 0 && a.D <= 256 && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) &&
-           al(a.k) && al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) && al(a.probs) &&
+    const bool src = a.probs ? al(a.probs) : (a.o && a.lse && al(a.o));
+    return src && a.D % 4 == 0 && a.D <= 256 && a.ts % 4 == 0 && a.bs % 4 == 0 && a.hs % 4 == 0 && al(a.q) &&
+           al(a.k) && al(a.v) && al(a.go) && al(a.dq) && al(a.dk) && al(a.dv) &&
            ((int64_t)(a.S + 64) * a.ts + a.D) * 4 < ((int64_t)1 << 31);
 }
 
+bool bwd_recompute_ok(const BwdArgs& a) { return a.o && a.lse && (bwd_tiled_ok(a) || bwd_wide_ok(a)); }
+
 bool bwd_uses_workspace(const BwdArgs& a) {
-    return a.probs && !(bwd_tiled_ok(a) && bh_enough(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
+    if (!a.probs) return !bwd_tiled_ok(a);  // recompute mode: the wide kernels pass Dq through it
+    return !(bwd_tiled_ok(a) && bh_enough(a) && (bwd::bh_ok(a) || bwd::bh_probs64_ok(a)));
 }
 
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
-    // recompute mode (no probs): tiled kernels only
-    if (!a.probs && (!a.o || !a.lse || !bwd_tiled_ok(a))) return hipErrorInvalidValue;
+    // recompute mode (no probs): the tiled kernels, or the wide ones with the Dq workspace
+    if (!a.probs && !(bwd_recompute_ok(a) && (bwd_tiled_ok(a) || a.dvec))) return hipErrorInvalidValue;
     if (bwd_tiled_ok(a)) {
         if (bh_enough(a) && bwd::bh_ok(a)) return bwd::launch_bh(a, s);
         if (bh_enough(a) && (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a))) return bwd::launch_bh64(a, s);

@@ -20,6 +20,12 @@
 // consecutive head dims across the lanes), so no transposed copies are
 // staged.  Dims D..DP-1 are zero in every operand.  Causal (probs zero above
 // the diagonal) skips tiles the same way bwd_tiled.h does.
+// Recompute mode (RECOMP; the probs-free pair): P is rebuilt per tile as
+// exp2(S' - lse'), S' = (scale log2 e) q.k formed like dP (a partial per
+// wave, summed through LDS; K, resp. Q, is already a row-major stage tile),
+// and Dq_i = dO_i . O_i.  The query-stationary kernel forms Dq from the rows
+// of dO and O, stores it to the B*H*S workspace for the key-stationary
+// kernel, and accumulates dQ = scale dS K directly.
 #pragma once
 
 #include "common.h"
@@ -38,13 +44,14 @@ using fa::halves_sum;
 // Workgroup: NQB query sub-blocks x DH dim slices; NBUF stage buffers (2:
 // the next stage goes to the other buffer during the MFMAs; 1: it waits in
 // registers and is stored after a barrier).
-template <int DP, int NQB, int DH, int NBUF, bool CAUSAL>
+template <int DP, int NQB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
 struct WideQ {
     using T = RowTiles<DP, DH>;
     static constexpr int NW = NQB * DH;
     static constexpr int NT = NW * 64;
     static constexpr int STAGE = 2 * T::ROW;  // V, K (row-major)
-    static constexpr int XCH = DH > 1 ? NW * 16 * 64 : 0;
+    static constexpr int NACC = RECOMP ? 1 : 2;  // accumulators: A (, Bm)
+    static constexpr int XCH = DH > 1 ? NW * 16 * 64 * (RECOMP ? 2 : 1) : 0;  // partial dP (, S') tiles
     static constexpr int LDS_FLOATS = NBUF * STAGE + XCH;
 
     __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int nqb, int bh, int rank) {
@@ -63,21 +70,45 @@ struct WideQ {
 
         float go[T::DW / 2];  // B operand of dP^T = V dO^T: dO[qi][wave's dims]
         T::load_lane_row(go, a.go + base, qi, S, D, a.ts, dh, hf);
+        // Recompute mode: Q (B operand of S'^T = K Q^T) in log2 units, the
+        // row's lse in the same units, and Dq_i = dO_i . O_i over every head
+        // dim (the same sum in each of the DH waves).
+        float q2[RECOMP ? T::DW / 2 : 1];
+        float lse2 = 0.f, dqv = 0.f;
+        if constexpr (RECOMP) {
+            T::load_lane_row(q2, a.q + base, qi, S, D, a.ts, dh, hf);
+            const float qsc = a.scale * kLog2e;
+#pragma unroll
+            for (int s2 = 0; s2 < T::DW / 2; ++s2) q2[s2] *= qsc;
+            float dsum = 0.f;
+            if (qi < S) {
+                const float* gp = a.go + base + (int64_t)qi * a.ts;
+                const float* op = a.o + base + (int64_t)qi * a.ts;
+                for (int d0 = hf * 4; d0 < D; d0 += 8) {
+                    const floatx4 g4 = *reinterpret_cast<const floatx4*>(gp + d0);
+                    const floatx4 o4 = *reinterpret_cast<const floatx4*>(op + d0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) dsum = fmaf(g4[j], o4[j], dsum);
+                }
+                lse2 = a.lse[(int64_t)bh * S + qi] * kLog2e;
+            }
+            dqv = halves_sum(dsum);
+        }
         RowLoader vl, kl;
         vl.init(a.v + base, a.ts, S, D);
         kl.init(a.k + base, a.ts, S, D);
         RowStage<DP, NT, 2> stg;
         floatx4* const xch = reinterpret_cast<floatx4*>(lds + NBUF * STAGE);
 
-        floatx16 acc[2][T::NDBW];  // A^T, Bm^T: [d][query]
+        floatx16 acc[NACC][T::NDBW];  // A^T (recompute: dS K), Bm^T: [d][query]
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+        for (int n = 0; n < NACC; ++n)
 #pragma unroll
             for (int db = 0; db < T::NDBW; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
         float ld = 0.f;
-        const float* prow = a.probs + ((int64_t)bh * S + qi) * S;
+        const float* prow = RECOMP ? nullptr : a.probs + ((int64_t)bh * S + qi) * S;
         const bool pvec = (S & 3) == 0;
         // P of key tile t in accumulator order (register 4g + j <-> key t*32 + 8g + 4h + j)
         auto load_p = [&](floatx4 (&pv)[4], int t) {
@@ -93,7 +124,7 @@ struct WideQ {
             }
         };
         floatx4 pnext[4];
-        if (wtiles > 0) load_p(pnext, 0);
+        if (!RECOMP && wtiles > 0) load_p(pnext, 0);
 
         if (nstages > 0) {
             stg.load(vl, kl, 0, D, tid);
@@ -107,13 +138,38 @@ struct WideQ {
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
-            if (act) T::dchain(dp, cur, go, c, hf, dh);  // (partial) dP^T, register r <-> key acc_key(r, h)
-            if constexpr (DH > 1) {
-                if (act) T::publish(dp, xch, wave, lane);
-                __syncthreads();
-                if (act) dp = T::total(dp, xch, sb, dh, lane);
-            }
+            floatx16 sc;  // recompute mode: S'^T, register r <-> key acc_key(r, h)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[r] = 0.f;
             if (act) {
+                T::dchain(dp, cur, go, c, hf, dh);  // (partial) dP^T, register r <-> key acc_key(r, h)
+                if (RECOMP) T::dchain(sc, cur + T::ROW, q2, c, hf, dh);
+            }
+            if constexpr (DH > 1) {
+                if (act) {
+                    T::publish(dp, xch, wave, lane);
+                    if (RECOMP) T::publish(sc, xch + NW * 256, wave, lane);
+                }
+                __syncthreads();
+                if (act) {
+                    dp = T::total(dp, xch, sb, dh, lane);
+                    if (RECOMP) sc = T::total(sc, xch + NW * 256, sb, dh, lane);
+                }
+            }
+            if constexpr (RECOMP) {
+                if (act) {
+                    const int kb0 = st * BK;
+                    const bool edge = kb0 + BK > S || (CAUSAL && kb0 + BK - 1 > qw0);
+                    floatx16 x;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kb0 + acc_key(r, hf);
+                        const float p = fast_exp2(sc[r] - lse2);
+                        x[r] = (!edge || (key < S && (!CAUSAL || key <= qi))) ? p * (dp[r] - dqv) : 0.f;
+                    }
+                    T::template rchain<1>(acc, cur + T::ROW, &x, c, hf, dh);  // (dS K)^T += K^T dS^T
+                }
+            } else if (act) {
                 floatx16 x[2];
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
@@ -141,7 +197,7 @@ struct WideQ {
             }
         }
 
-        const float dq = halves_sum(ld);
+        const float dq = RECOMP ? dqv : halves_sum(ld);
         if (qi < S) {
             if (dh == 0 && hf == 0) a.dvec[(int64_t)bh * S + qi] = dq;
             float* out = a.dq + base + (int64_t)qi * a.ts;
@@ -153,7 +209,9 @@ struct WideQ {
                     if (d0 < D) {
                         floatx4 v;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) v[j] = a.scale * fmaf(-dq, acc[1][db][4 * g + j], acc[0][db][4 * g + j]);
+                        for (int j = 0; j < 4; ++j)
+                            v[j] = RECOMP ? a.scale * acc[0][db][4 * g + j]
+                                          : a.scale * fmaf(-dq, acc[NACC - 1][db][4 * g + j], acc[0][db][4 * g + j]);
                         *reinterpret_cast<floatx4*>(out + d0) = v;
                     }
                 }
@@ -162,14 +220,15 @@ struct WideQ {
 };
 
 // ----------------------------------------------------------------- dK, dV
-template <int DP, int NKB, int DH, int NBUF, bool CAUSAL>
+template <int DP, int NKB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
 struct WideKV {
     using T = RowTiles<DP, DH>;
     static constexpr int NW = NKB * DH;
     static constexpr int NT = NW * 64;
     static constexpr int DQ_OFF = 2 * T::ROW;
-    static constexpr int STAGE = 2 * T::ROW + BK;  // dO, Q (row-major), Dq
-    static constexpr int XCH = DH > 1 ? NW * 16 * 64 : 0;
+    static constexpr int LSE_OFF = DQ_OFF + BK;
+    static constexpr int STAGE = 2 * T::ROW + BK + (RECOMP ? BK : 0);  // dO, Q (row-major), Dq (, lse')
+    static constexpr int XCH = DH > 1 ? NW * 16 * 64 * (RECOMP ? 2 : 1) : 0;  // partial dP (, S') tiles
     static constexpr int LDS_FLOATS = NBUF * STAGE + XCH;
     static_assert(STAGE % 4 == 0, "16-byte aligned stage buffers");
 
@@ -190,11 +249,20 @@ struct WideKV {
 
         float vr[T::DW / 2];  // B operand of dP = dO V^T: V[kj][wave's dims]
         T::load_lane_row(vr, a.v + base, kj, S, D, a.ts, dh, hf);
+        // Recompute mode: K (B operand of S' = Q K^T) in log2 units
+        float kr2[RECOMP ? T::DW / 2 : 1];
+        if constexpr (RECOMP) {
+            T::load_lane_row(kr2, a.k + base, kj, S, D, a.ts, dh, hf);
+            const float qsc = a.scale * kLog2e;
+#pragma unroll
+            for (int s2 = 0; s2 < T::DW / 2; ++s2) kr2[s2] *= qsc;
+        }
         RowLoader gl, ql;
         gl.init(a.go + base, a.ts, S, D);
         ql.init(a.q + base, a.ts, S, D);
         RowStage<DP, NT, 2> stg;
         float dqs = 0.f;
+        float lses = 0.f;  // recompute mode: lse' of the staged row (+inf past the last row: P = 0)
         floatx4* const xch = reinterpret_cast<floatx4*>(lds + NBUF * STAGE);
 
         floatx16 acc[2][T::NDBW];  // dV^T, dK^T (unscaled): [d][key]
@@ -204,7 +272,7 @@ struct WideKV {
             for (int db = 0; db < T::NDBW; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[n][db][r] = 0.f;
-        const float* pcol = a.probs + (int64_t)bh * S * S + kj;
+        const float* pcol = RECOMP ? nullptr : a.probs + (int64_t)bh * S * S + kj;
         // P column of query tile it, register r <-> query it*32 + acc_key(r, h)
         auto load_p = [&](floatx16& pv, int it) {
 #pragma unroll
@@ -216,14 +284,20 @@ struct WideKV {
         auto load = [&](int st) {
             const int row0 = (it0 + st) * BK;
             stg.load(gl, ql, row0, D, tid);
-            if (tid < BK) dqs = row0 + tid < S ? a.dvec[(int64_t)bh * S + row0 + tid] : 0.f;
+            if (tid < BK) {
+                dqs = row0 + tid < S ? a.dvec[(int64_t)bh * S + row0 + tid] : 0.f;
+                if (RECOMP) lses = row0 + tid < S ? a.lse[(int64_t)bh * S + row0 + tid] * kLog2e : kInf;
+            }
         };
         auto store = [&](float* dst) {
             stg.store(dst, T::ROW, tid);
-            if (tid < BK) dst[DQ_OFF + tid] = dqs;
+            if (tid < BK) {
+                dst[DQ_OFF + tid] = dqs;
+                if (RECOMP) dst[LSE_OFF + tid] = lses;
+            }
         };
         floatx16 pnext;
-        if (wit0 < nq) load_p(pnext, wit0);
+        if (!RECOMP && wit0 < nq) load_p(pnext, wit0);
 
         if (nstages > 0) {
             load(0);
@@ -238,16 +312,43 @@ struct WideKV {
             floatx16 dp;
 #pragma unroll
             for (int r = 0; r < 16; ++r) dp[r] = 0.f;
-            if (act) T::dchain(dp, cur, vr, c, hf, dh);  // (partial) dP, register r <-> query acc_key(r, h)
+            floatx16 sc;  // recompute mode: S', register r <-> query acc_key(r, h)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+            if (act) {
+                T::dchain(dp, cur, vr, c, hf, dh);  // (partial) dP, register r <-> query acc_key(r, h)
+                if (RECOMP) T::dchain(sc, cur + T::ROW, kr2, c, hf, dh);
+            }
             if constexpr (DH > 1) {
-                if (act) T::publish(dp, xch, wave, lane);
+                if (act) {
+                    T::publish(dp, xch, wave, lane);
+                    if (RECOMP) T::publish(sc, xch + NW * 256, wave, lane);
+                }
                 __syncthreads();
-                if (act) dp = T::total(dp, xch, sb, dh, lane);
+                if (act) {
+                    dp = T::total(dp, xch, sb, dh, lane);
+                    if (RECOMP) sc = T::total(sc, xch + NW * 256, sb, dh, lane);
+                }
             }
             if (act) {
                 floatx16 x[2];  // P, dS
-                x[0] = pnext;
-                if (it + 1 < nq) load_p(pnext, it + 1);
+                if constexpr (RECOMP) {
+                    // causal: some query of this tile precedes some key of the wave
+                    const bool edge = CAUSAL && it * BK < kw0 + BK - 1;
+                    const float* lt = cur + LSE_OFF;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const floatx4 l4 = *reinterpret_cast<const floatx4*>(lt + 8 * g + 4 * hf);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float p = fast_exp2(sc[4 * g + j] - l4[j]);
+                            x[0][4 * g + j] = (!edge || it * BK + 8 * g + 4 * hf + j >= kj) ? p : 0.f;
+                        }
+                    }
+                } else {
+                    x[0] = pnext;
+                    if (it + 1 < nq) load_p(pnext, it + 1);
+                }
                 const float* dqt = cur + DQ_OFF;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -290,17 +391,17 @@ struct WideKV {
     }
 };
 
-template <int DP, int NQB, int DH, int NBUF, bool CAUSAL>
+template <int DP, int NQB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
 __global__ __launch_bounds__(NQB* DH * 64) void bwd_wide_q_kernel(BwdArgs a, int nqb) {
-    using K = WideQ<DP, NQB, DH, NBUF, CAUSAL>;
+    using K = WideQ<DP, NQB, DH, NBUF, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     const int BH = a.B * a.H;
     K::run(a, lds, nqb, blockIdx.x % BH, blockIdx.x / BH);
 }
 
-template <int DP, int NKB, int DH, int NBUF, bool CAUSAL>
+template <int DP, int NKB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
 __global__ __launch_bounds__(NKB* DH * 64) void bwd_wide_kv_kernel(BwdArgs a, int nkb) {
-    using K = WideKV<DP, NKB, DH, NBUF, CAUSAL>;
+    using K = WideKV<DP, NKB, DH, NBUF, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     const int BH = a.B * a.H;
     K::run(a, lds, nkb, blockIdx.x % BH, blockIdx.x / BH);
@@ -309,24 +410,30 @@ __global__ __launch_bounds__(NKB* DH * 64) void bwd_wide_kv_kernel(BwdArgs a, in
 // Both kernels of one problem (the second reads the first's Dq).  Blocks
 // b run (b, h) = b mod B*H at launch rank b / B*H: the heaviest causal blocks
 // of every (b, h) first.
-template <int DP, int NB, int DH, int NBUF, bool CAUSAL>
+template <int DP, int NB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
 hipError_t launch_wide_mode(const BwdArgs& a, hipStream_t s) {
     const int BH = a.B * a.H;
     const int nb = (a.S + NB * BK - 1) / (NB * BK);
     const int64_t g = (int64_t)nb * BH;
     if (g <= 0 || g > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((bwd_wide_q_kernel<DP, NB, DH, NBUF, CAUSAL>), dim3((unsigned)g), dim3(NB * DH * 64), 0, s, a,
-                       nb);
+    hipLaunchKernelGGL((bwd_wide_q_kernel<DP, NB, DH, NBUF, CAUSAL, RECOMP>), dim3((unsigned)g), dim3(NB * DH * 64), 0,
+                       s, a, nb);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_wide_kv_kernel<DP, NB, DH, NBUF, CAUSAL>), dim3((unsigned)g), dim3(NB * DH * 64), 0, s,
-                       a, nb);
+    hipLaunchKernelGGL((bwd_wide_kv_kernel<DP, NB, DH, NBUF, CAUSAL, RECOMP>), dim3((unsigned)g), dim3(NB * DH * 64),
+                       0, s, a, nb);
     return hipGetLastError();
 }
 
+// Stored probs, or (probs == nullptr) recompute mode from a.o and a.lse; both
+// need the B*H*S workspace a.dvec.
 template <int DP, int NB, int DH, int NBUF>
 hipError_t launch_wide(const BwdArgs& a, hipStream_t s) {
-    return a.causal ? launch_wide_mode<DP, NB, DH, NBUF, true>(a, s) : launch_wide_mode<DP, NB, DH, NBUF, false>(a, s);
+    if (!a.probs)
+        return a.causal ? launch_wide_mode<DP, NB, DH, NBUF, true, true>(a, s)
+                        : launch_wide_mode<DP, NB, DH, NBUF, false, true>(a, s);
+    return a.causal ? launch_wide_mode<DP, NB, DH, NBUF, true, false>(a, s)
+                    : launch_wide_mode<DP, NB, DH, NBUF, false, false>(a, s);
 }
 
 }  // namespace bwd

@@ -74,11 +74,13 @@ struct BwdArgs {
     int resident;
 };
 hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s);
-// The LDS-tiled MFMA kernels apply (D = 32 or 64, 16-byte aligned rows); the
-// only backward path for recompute mode.
+// The per-wave LDS-tiled MFMA kernels apply (D = 32 or 64, 16-byte aligned rows).
 bool bwd_tiled_ok(const BwdArgs& a);
+// Recompute mode (a.o, a.lse, no probs) has a kernel: the tiled ones, or the
+// head-dim-split ones (D % 4 == 0 up to 256, 16-byte aligned rows).
+bool bwd_recompute_ok(const BwdArgs& a);
 // False when launch_attn_bwd takes a path that needs no dvec workspace (the
-// one-workgroup-per-(b, h) kernel, or recompute mode).
+// one-workgroup-per-(b, h) kernels, or recompute mode at D = 32 / 64).
 bool bwd_uses_workspace(const BwdArgs& a);
 
 // Unfused single-head helpers (HipGPT src/hip_kernels.cpp:454-532).

@@ -88,9 +88,11 @@ int hipgpt_attn_bwd_qkv_planar_noalloc(const float* grad_out, const float* qkv,
  *             query i sees (all, or j <= i when causal).
  *   backward: grad_out, qkv, the forward's out and lse -> every element of
  *             the planar grad_qkv [dQ|dK|dV]; P is recomputed per tile.
- *             workspace / workspace_bytes are ignored (may be NULL / 0).
- * fp32, D = E/H of 32 or 64, 16-byte aligned buffers; other shapes return
- * HIPGPT_ERR_UNSUPPORTED. */
+ *             At D = 32 and 64 workspace / workspace_bytes are ignored (may
+ *             be NULL / 0); other head dims need the B*H*S floats of
+ *             hipgpt_attn_bwd_workspace_bytes (else HIPGPT_ERR_WORKSPACE).
+ * fp32, D = E/H a multiple of 4 up to 256, 16-byte aligned buffers; other
+ * shapes return HIPGPT_ERR_UNSUPPORTED. */
 int hipgpt_attn_fwd_lse_qkv_planar(const float* d_qkv, float* d_output,
                                    float* lse, int B, int S, int E, int H,
                                    int causal, hipStream_t stream);

@@ -78,15 +78,19 @@ def test_strerror_and_host_validation():
     assert L.hipgpt_attn_bwd_workspace_bytes(2, 8, 3) == 2 * 3 * 8 * 4
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 64, 2, 0, None, 0, None) == _lib.ERR_WORKSPACE
     assert L.hipgpt_attn_bwd_qkv_planar(p, p, p, p, 1, 8, 63, 2, 0, p, 1 << 20, None) == _lib.ERR_INVALID
-    # probs-free training pair: null lse/out, bad split, D other than 32/64, unaligned, missing workspace
+    # probs-free training pair: null lse/out, bad split, D not a multiple of 4 or above 256, unaligned,
+    # missing workspace (head dims other than 32 / 64)
     fl, bl = L.hipgpt_attn_fwd_lse_qkv_planar, L.hipgpt_attn_bwd_lse_qkv_planar
     assert fl(p, p, None, 1, 8, 64, 2, 1, None) == _lib.ERR_INVALID
     assert fl(p, p, p, 1, 8, 63, 2, 1, None) == _lib.ERR_INVALID
-    assert fl(p, p, p, 1, 8, 96, 2, 1, None) == _lib.ERR_UNSUPPORTED   # D = 48
+    assert fl(p, p, p, 1, 8, 100, 2, 1, None) == _lib.ERR_UNSUPPORTED   # D = 50
+    assert fl(p, p, p, 1, 8, 520, 2, 1, None) == _lib.ERR_UNSUPPORTED   # D = 260
     assert fl(p + 4, p, p, 1, 8, 64, 2, 1, None) == _lib.ERR_UNSUPPORTED  # qkv not 16-byte aligned
     assert bl(p, p, None, p, p, 1, 8, 64, 2, 1, p, 1 << 20, None) == _lib.ERR_INVALID
     assert bl(p, p, p, None, p, 1, 8, 64, 2, 1, p, 1 << 20, None) == _lib.ERR_INVALID
-    assert bl(p, p, p, p, p, 1, 8, 256, 2, 1, p, 1 << 20, None) == _lib.ERR_UNSUPPORTED  # D = 128
+    assert bl(p, p, p, p, p, 1, 8, 100, 2, 1, p, 1 << 20, None) == _lib.ERR_UNSUPPORTED  # D = 50
+    assert bl(p, p, p, p, p, 1, 8, 256, 2, 1, None, 0, None) == _lib.ERR_WORKSPACE  # D = 128
+    assert bl(p, p, p, p, p, 1, 8, 256, 2, 1, p, 2 * 8 * 4 - 4, None) == _lib.ERR_WORKSPACE
     # KV-cache decode: null lens / caches, bad sizes, unsupported D, missing workspace
     kvc = L.hipgpt_attn_decode_kvcache
     z11 = [0] * 11

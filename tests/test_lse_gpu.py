@@ -85,6 +85,29 @@ def test_lse_pair_matches_oracle(dev, B, S, E, H, causal):
     assert np.abs(got - want_g).max() <= tol(want_g)
 
 
+# Head dims other than 32 / 64 (multiples of 4 up to 256): the forward's
+# padded kernels (D = 16, 48, 80: padded to 32, 64, 128), D = 128 and the
+# head-dim-split forward above 128; the backward's head-dim-split kernels,
+# which pass the row dots dO . O through the B*H*S workspace.
+WIDE_SHAPES = [(2, 40, 32, 2), (1, 70, 96, 2), (2, 33, 160, 2), (1, 130, 256, 2), (2, 100, 384, 3),
+               (1, 257, 256, 1), (1, 64, 320, 2), (2, 150, 512, 2), (1, 1, 256, 2)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,S,E,H", WIDE_SHAPES)
+def test_lse_pair_other_head_dims(dev, B, S, E, H, causal):
+    qkv = O.seeded_planar(0x57 + B * 131 + S * 7 + E, B, S, E)
+    go = O.fill_normal(0x58 + S + E, B * S * E)
+    _, out, lse, grad = run_pair(qkv, go, B, S, E, H, causal)
+    assert np.abs(host(lse) - lse_f64(qkv, B, S, E, H, causal)).max() <= 1e-5
+    want_o, probs = O.launch_multihead_attention(qkv, B, S, E, H, causal=causal, want_probs=True)
+    assert np.abs(host(out).reshape(-1) - want_o.reshape(-1)).max() <= 1e-4
+    want_g = O.mha_backward(go, qkv, probs, B, S, E, H)
+    got = host(grad)
+    assert np.isfinite(got).all()  # every element written
+    assert np.abs(got - want_g).max() <= tol(want_g)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_lse_pair_matches_probs_backward_and_autograd(dev, causal):
     B, S, E, H = 2, 80, 256, 4
@@ -113,10 +136,12 @@ def test_lse_pair_matches_probs_backward_and_autograd(dev, causal):
     assert np.abs(g1 - want).max() <= tol(want)
 
 
-@pytest.mark.parametrize("cfg,shape", [("c1", (32, 256, 256, 8)), ("c2", (32, 256, 512, 8))])
+@pytest.mark.parametrize("cfg,shape", [("c1", (32, 256, 256, 8)), ("c2", (32, 256, 512, 8)),
+                                       ("c3", (8, 1024, 768, 12)), ("c4", (4, 2048, 2048, 16))])
 def test_lse_pair_baseline_configs(dev, cfg, shape):
-    """Full c1 / c2 shapes (causal): the probs-free gradients equal the
-    probs-based backward's on the same forward."""
+    """Full c1 .. c4 shapes (causal): the probs-free gradients equal the
+    probs-based backward's on the same forward (c4: D = 128, the head-dim-split
+    backward)."""
     B, S, E, H = shape
     qkv = O.seeded_planar(91 + E, B, S, E)
     go = O.fill_normal(92 + E, B * S * E)
