@@ -310,18 +310,7 @@ hipError_t launch_dp(const BwdArgs& a, hipStream_t s) {
 // key-stationary NKB x NQS.  4 x 1 for both was best or within 3% of the
 // best of nine shapes on MI355X for the c1 causal, c1 non-causal and c2
 // causal backward.
-#ifndef HIPGPT_BWDQ_NQS
-#define HIPGPT_BWDQ_NQS 4
-#endif
-#ifndef HIPGPT_BWDQ_NKS
-#define HIPGPT_BWDQ_NKS 1
-#endif
-#ifndef HIPGPT_BWDKV_NKB
-#define HIPGPT_BWDKV_NKB 4
-#endif
-#ifndef HIPGPT_BWDKV_NQS
-#define HIPGPT_BWDKV_NQS 1
-#endif
+constexpr int kBwdQNqs = 4, kBwdQNks = 1, kBwdKvNkb = 4, kBwdKvNqs = 1;
 
 hipError_t bwd_wait_expired(unsigned int* count, bool clear) { return wait_expired_take(count, clear); }
 
@@ -368,8 +357,8 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
         if (bh_enough(a) && bwd::bh_ok(a)) return bwd::launch_bh(a, s);
         if (bh_enough(a) && (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a))) return bwd::launch_bh64(a, s);
         if (a.D == 32)
-            return bwd::launch_tiled<32, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
-        return bwd::launch_tiled<64, HIPGPT_BWDQ_NQS, HIPGPT_BWDQ_NKS, HIPGPT_BWDKV_NKB, HIPGPT_BWDKV_NQS>(a, s);
+            return bwd::launch_tiled<32, kBwdQNqs, kBwdQNks, kBwdKvNkb, kBwdKvNqs>(a, s);
+        return bwd::launch_tiled<64, kBwdQNqs, kBwdQNks, kBwdKvNkb, kBwdKvNqs>(a, s);
     }
     if (bwd_wide_ok(a)) {
         if (a.D <= 32) return bwd::launch_wide<32, 4, 1, 2>(a, s);

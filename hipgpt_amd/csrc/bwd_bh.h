@@ -68,9 +68,7 @@ constexpr int CPR = D / 4;     // 16-byte chunks per row
 constexpr int kSpinMax = 1 << 20;  // bound of a flag wait (~0.1 s)
 
 // HBM bytes per s_memrealtime tick (10 ns) assumed by the staggered start.
-#ifndef HIPGPT_BH_SLOT_DIV
-#define HIPGPT_BH_SLOT_DIV 60000
-#endif
+constexpr unsigned long long kSlotDiv = 60000;
 
 // LDS layout in floats for Sp = S rounded up to 32 rows.
 struct Layout {
@@ -118,14 +116,8 @@ __device__ __forceinline__ int dq_key(int s, int h) { return 16 * (s >> 3) + 8 *
 // through the wave's scratch X (pitch XP), non-temporally; rows past S are
 // dropped.  X must be free: its earlier reads issued (a wave's LDS accesses
 // run in order; the memory clobbers keep the compiler's order).
-#ifndef HIPGPT_BWD_ROWS_T
-#define HIPGPT_BWD_ROWS_T 1
-#endif
-// Cache policy of the dQ row stores (whole rows already): 2 = non-temporal.
-#ifndef HIPGPT_DQ_NT
-#define HIPGPT_DQ_NT 1
-#endif
-constexpr int kDqPolicy = HIPGPT_DQ_NT ? 2 : 0;
+// Cache policy of the dQ row stores (whole rows already): non-temporal.
+constexpr int kDqPolicy = 2;
 __device__ __forceinline__ void store_rows_t(float* X, float* dst0, const floatx16& acc, float mul, int row0, int S,
                                              int64_t ts, int lane) {
     const int c = lane & 31, hf = lane >> 5;
@@ -147,10 +139,7 @@ __device__ __forceinline__ void store_rows_t(float* X, float* dst0, const floatx
 
 // Stored-probs loads of the single-read kernels (each P element read once):
 // non-temporal (c1 drop-in backward 52.2 -> 50.6 us cache-rotated).
-#ifndef HIPGPT_P_NT
-#define HIPGPT_P_NT 1
-#endif
-constexpr int kPPolicy = HIPGPT_P_NT ? 2 : 0;
+constexpr int kPPolicy = 2;
 __device__ __forceinline__ void load_p_tile(floatx16& pv, __amdgpu_buffer_rsrc_t pr, int i, int kj, bool kval, int hf,
                                             int S) {
     const int S4 = S * 4;
@@ -215,7 +204,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // loads in a burst; later ones start as slots free up and are not delayed.
     if (!PROBS && CAUSAL && kt > 0 && bhi < a.resident) {
         constexpr int kWaveBytes = 5 * BK * D * 4;  // Q, dO, O rows + K, V rows
-        const unsigned long long slot = (unsigned long long)a.resident * kWaveBytes / HIPGPT_BH_SLOT_DIV;
+        const unsigned long long slot = (unsigned long long)a.resident * kWaveBytes / kSlotDiv;
         const unsigned long long until = t_start + slot * kt;
         for (int n = 0; n < 4096 && __builtin_amdgcn_s_memrealtime() < until; ++n) __builtin_amdgcn_s_sleep(2);
     }
@@ -529,22 +518,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     for (int t = 1; t < nsteps; ++t) job(std::true_type{}, t);
     chain_add(dq_term(), iprev, nsteps - 1);
 
-    if (HIPGPT_BWD_ROWS_T) {
-        // dV, dK through the wave's scratch (its last reads were issued
-        // above): whole 128-byte rows, non-temporal
-        store_rows_t(X, a.dv + base + (int64_t)(kt * BK) * a.ts, accv, 1.f, kt * BK, S, a.ts, lane);
-        store_rows_t(X, a.dk + base + (int64_t)(kt * BK) * a.ts, acck, a.scale, kt * BK, S, a.ts, lane);
-    } else if (kval) {
-        float* dvp = a.dv + base + (int64_t)kj * a.ts;
-        float* dkp = a.dk + base + (int64_t)kj * a.ts;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 8 * g + 4 * hf;
-            *reinterpret_cast<floatx4*>(dvp + d0) = floatx4{accv[4 * g], accv[4 * g + 1], accv[4 * g + 2], accv[4 * g + 3]};
-            *reinterpret_cast<floatx4*>(dkp + d0) = floatx4{a.scale * acck[4 * g], a.scale * acck[4 * g + 1],
-                                                            a.scale * acck[4 * g + 2], a.scale * acck[4 * g + 3]};
-        }
-    }
+    // dV, dK through the wave's scratch (its last reads were issued above):
+    // whole 128-byte rows, non-temporal
+    store_rows_t(X, a.dv + base + (int64_t)(kt * BK) * a.ts, accv, 1.f, kt * BK, S, a.ts, lane);
+    store_rows_t(X, a.dk + base + (int64_t)(kt * BK) * a.ts, acck, a.scale, kt * BK, S, a.ts, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -836,19 +813,9 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
         reduce_dq(Even{}, t);
     }
 
-    if (HIPGPT_BWD_ROWS_T && active) {
+    if (active) {
         store_rows_t(X, a.dv + base + (int64_t)(wave * BK) * a.ts, accv, 1.f, wave * BK, S, a.ts, lane);
         store_rows_t(X, a.dk + base + (int64_t)(wave * BK) * a.ts, acck, a.scale, wave * BK, S, a.ts, lane);
-    } else if (active && kval) {
-        float* dvp = a.dv + base + (int64_t)kj * a.ts;
-        float* dkp = a.dk + base + (int64_t)kj * a.ts;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 8 * g + 4 * hf;
-            *reinterpret_cast<floatx4*>(dvp + d0) = floatx4{accv[4 * g], accv[4 * g + 1], accv[4 * g + 2], accv[4 * g + 3]};
-            *reinterpret_cast<floatx4*>(dkp + d0) = floatx4{a.scale * acck[4 * g], a.scale * acck[4 * g + 1],
-                                                            a.scale * acck[4 * g + 2], a.scale * acck[4 * g + 3]};
-        }
     }
 }
 
@@ -894,12 +861,6 @@ hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Stored probs without a causal mask: the single-read kernel (1) or the
-// two-phase kernel (0).
-#ifndef HIPGPT_BH_SINGLE_READ
-#define HIPGPT_BH_SINGLE_READ 1
-#endif
-
 inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -911,7 +872,8 @@ inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
 }
 
 inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
-    if (a.probs && !a.causal && HIPGPT_BH_SINGLE_READ) return launch_bh_probs(a, s);
+    // stored probs without a causal mask: the single-read kernel
+    if (a.probs && !a.causal) return launch_bh_probs(a, s);
     if (a.probs) return a.causal ? launch_bh_mode<true, true>(a, s) : launch_bh_mode<false, true>(a, s);
     return a.causal ? launch_bh_mode<true, false>(a, s) : launch_bh_mode<false, false>(a, s);
 }

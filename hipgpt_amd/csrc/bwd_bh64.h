@@ -418,7 +418,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
     if (t < nt) step(Even{}, t, p);
     reduce_dq(nt - 1);
 
-    if (HIPGPT_BWD_ROWS_T && active) {
+    if (active) {
         // dV, dK through the wave's scratch, one 32-dim block at a time: whole
         // 128-byte row segments, non-temporal (the scratch's last reads, the
         // dQ term's operands, were issued before the closing barrier)
@@ -428,20 +428,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
             store_rows_t(X, a.dk + base + (int64_t)(wave * BK) * a.ts + 32 * n, acck[n], a.scale, wave * BK, S, a.ts,
                          lane);
         }
-    } else if (active && kval) {
-        float* dvp = a.dv + base + (int64_t)kj * a.ts;
-        float* dkp = a.dk + base + (int64_t)kj * a.ts;
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d0 = 32 * n + 8 * g + 4 * hf;
-                *reinterpret_cast<floatx4*>(dvp + d0) =
-                    floatx4{accv[n][4 * g], accv[n][4 * g + 1], accv[n][4 * g + 2], accv[n][4 * g + 3]};
-                *reinterpret_cast<floatx4*>(dkp + d0) =
-                    floatx4{a.scale * acck[n][4 * g], a.scale * acck[n][4 * g + 1], a.scale * acck[n][4 * g + 2],
-                            a.scale * acck[n][4 * g + 3]};
-            }
     }
 }
 
@@ -451,18 +437,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh64_kernel(BwdArgs a) {
 // (checked by the caller).  Stored probs are read as single floats, so there
 // is no condition on S or on the probs' alignment; without them the forward's
 // O and lse are required (the caller checks that too).
-#ifndef HIPGPT_BH_PROBS_D64
-#define HIPGPT_BH_PROBS_D64 1
-#endif
-#ifndef HIPGPT_BH_LSE_D64
-#define HIPGPT_BH_LSE_D64 1
-#endif
 inline bool bh_probs64_ok(const BwdArgs& a) {
-    return HIPGPT_BH_PROBS_D64 && a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS;
+    return a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS;
 }
-inline bool bh_lse64_ok(const BwdArgs& a) {
-    return HIPGPT_BH_LSE_D64 && !a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS;
-}
+inline bool bh_lse64_ok(const BwdArgs& a) { return !a.probs && a.D == bh::p64::DK && a.S >= 1 && a.S <= bh::MAXS; }
 
 inline hipError_t launch_bh64(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;

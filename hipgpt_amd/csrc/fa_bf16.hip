@@ -133,24 +133,11 @@ struct B16Traits {
 // Workgroup shape: 4 query sub-blocks share each K/V stage (bf16 tiles are
 // short on the matrix cores, so the stage's loads, LDS stores and barrier
 // are amortised over more work); 4 x 2 measured best of 2x2, 4x1, 4x2, 2x4, 8x1.
-#ifndef HIPGPT_BF16_NQS
-#define HIPGPT_BF16_NQS 4
-#endif
-#ifndef HIPGPT_BF16_NKS
-#define HIPGPT_BF16_NKS 2
-#endif
-// Prefetch depth in stages (1 or 2); one measured best at every D.
-#ifndef HIPGPT_BF16_PF
-#define HIPGPT_BF16_PF 1
-#endif
-#ifndef HIPGPT_BF16_D128_PF
-#define HIPGPT_BF16_D128_PF 1
-#endif
+constexpr int kNqs = 4, kNks = 2;
 
 template <int D>
 hipError_t launch_d(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
-    constexpr int PF = D > 64 ? HIPGPT_BF16_D128_PF : HIPGPT_BF16_PF;
-    return fa::launch_fa_flags<B16Traits<D>, HIPGPT_BF16_NQS, HIPGPT_BF16_NKS, PF, true>(a, causal, probs, s);
+    return fa::launch_fa_flags<B16Traits<D>, kNqs, kNks, true>(a, causal, probs, s);
 }
 
 }  // namespace

@@ -132,14 +132,6 @@ __device__ __forceinline__ void store_probs_tile(float* prow, const floatx16& p,
     }
 }
 
-// Causal probs, streaming kernel: the zeros above the diagonal are stored
-// before the sweeps (1; c1 with probs 26.5 -> 25.2 us) or after them (0).  The
-// resident kernel stores them last: its start is already HBM-bound, and
-// storing them first measured slower there (c2 with probs 46.7 -> 48.3 us).
-#ifndef HIPGPT_ZERO_FIRST
-#define HIPGPT_ZERO_FIRST 1
-#endif
-
 // Causal: zero the probs of this wave's queries for keys >= z0 (whole rows
 // per instruction; non-temporal if NT: the score-resident streaming sweep,
 // c1 with probs 27.7 -> 26.6 us; the other probs paths measured 1-9% slower

@@ -157,40 +157,10 @@ struct F32Traits {
 // measured on MI355X with waves ranked by SIMD: D=32 2x2 (c1), D=64 4x2 (c3),
 // D=128 8x1 (c4) -- the larger head dims run 2 waves per SIMD, and more query
 // sub-blocks per workgroup share each K/V stage.
-#ifndef HIPGPT_F32_D32_NQS
-#define HIPGPT_F32_D32_NQS 2
-#endif
-#ifndef HIPGPT_F32_D32_NKS
-#define HIPGPT_F32_D32_NKS 2
-#endif
-#ifndef HIPGPT_F32_D64_NQS
-#define HIPGPT_F32_D64_NQS 4
-#endif
-#ifndef HIPGPT_F32_D64_NKS
-#define HIPGPT_F32_D64_NKS 2
-#endif
-#ifndef HIPGPT_F32_D128_NQS
-#define HIPGPT_F32_D128_NQS 8
-#endif
-#ifndef HIPGPT_F32_D128_NKS
-#define HIPGPT_F32_D128_NKS 1
-#endif
-// Prefetch depth in stages (1 or 2) per padded head dim; one measured best
-// (two costs an occupancy step at DP = 32 and gains nothing elsewhere).
-#ifndef HIPGPT_F32_D32_PF
-#define HIPGPT_F32_D32_PF 1
-#endif
-#ifndef HIPGPT_F32_D64_PF
-#define HIPGPT_F32_D64_PF 1
-#endif
-#ifndef HIPGPT_F32_D128_PF
-#define HIPGPT_F32_D128_PF 1
-#endif
-
-template <int DP, int NQS, int NKS, int PF>
+template <int DP, int NQS, int NKS>
 hipError_t launch_dp(const AttnArgs& a, bool causal, bool probs, bool vec, hipStream_t s) {
-    return vec ? fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, PF, true>(a, causal, probs, s)
-               : fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, PF, false>(a, causal, probs, s);
+    return vec ? fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, true>(a, causal, probs, s)
+               : fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, false>(a, causal, probs, s);
 }
 
 }  // namespace
@@ -206,15 +176,9 @@ int fa_f32_padded_dim(int D) {
 
 // Short sequences at DP = 64 (all K/V tiles of a (b, h) fit one workgroup's
 // LDS) run the resident kernel: 8 waves = 256 queries per workgroup.  At
-// DP = 32 the streaming kernel measured faster (its four waves per SIMD hide
-// the short tiles' softmax better), so the resident path is off there unless
-// HIPGPT_RES_D32_NKS is set to 1 or 2 at build time.
-#ifndef HIPGPT_RESIDENT_MAX_SQ
-#define HIPGPT_RESIDENT_MAX_SQ 256
-#endif
-#ifndef HIPGPT_RES_D32_NKS
-#define HIPGPT_RES_D32_NKS 0
-#endif
+// DP = 32 the streaming kernel measured faster (17.2 against 17.5 us at c1:
+// its four waves per SIMD hide the short tiles' softmax better).
+constexpr int kResidentMaxSq = 256;
 
 // Small D <= 32 problems (at most 128 query tiles of 32 rows in all, 128 to
 // 256 keys -- HipGPT's generation call, B = 1, H = 8, S = 256, is 64 tiles):
@@ -223,80 +187,51 @@ int fa_f32_padded_dim(int D) {
 // stages of key tiles each, scores kept in registers with probs).  The
 // generation call 12.6 -> 9.2 us, B = 1 causal 9.5 -> 7.5 us; from 256 query
 // tiles on the two shapes measure the same, and below 128 keys a split would
-// hold no tile.
-#ifndef HIPGPT_F32_SMALL
-#define HIPGPT_F32_SMALL 1
-#endif
-#ifndef HIPGPT_F32_SMALL_NQS
-#define HIPGPT_F32_SMALL_NQS 1
-#endif
-#ifndef HIPGPT_F32_SMALL_NKS
-#define HIPGPT_F32_SMALL_NKS 4
-#endif
+// hold no tile.  (1 x 8 measured 9.4 us on the generation call, 1 x 2 12.3,
+// 2 x 4 12.5.)
+constexpr int kSmallNqs = 1, kSmallNks = 4, kSmallMaxQtiles = 128;
 // The same split at D = 64 replaces the resident kernel (one 8-wave
 // workgroup per (b, h), latency-bound when B*H is far below the CU count)
 // up to 512 query tiles: the generation call at E = 512 (B = 1, H = 8,
 // S = 256, drop-in) 47.1 -> 12.8 us, B = 8 drop-in 52.0 -> 26.9 us, B = 8
 // causal 29.8 -> 20.3 us; at B = 16 (1024 tiles) the causal resident kernel
 // is faster (31.0 against 38.7 us).
-#ifndef HIPGPT_F32_SMALL64
-#define HIPGPT_F32_SMALL64 1
-#endif
-#ifndef HIPGPT_F32_SMALL64_MAX_QTILES
-#define HIPGPT_F32_SMALL64_MAX_QTILES 512
-#endif
-#ifndef HIPGPT_F32_SMALL_MAX_QTILES
-#define HIPGPT_F32_SMALL_MAX_QTILES 128
-#endif
+constexpr int kSmall64MaxQtiles = 512;
 
 hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t stream) {
     const bool probs = a.probs != nullptr;
-#if HIPGPT_F32_SMALL
     {
-        constexpr int NQ = HIPGPT_F32_SMALL_NQS, NK = HIPGPT_F32_SMALL_NKS, ST = 8 / NK;
+        constexpr int NQ = kSmallNqs, NK = kSmallNks, ST = 8 / NK;
         using TS = F32Traits<32, true, ST>;
         const int64_t qtiles = (int64_t)a.B * a.H * ((a.Sq + 31) / 32);
-        const bool small = vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= HIPGPT_F32_SMALL_MAX_QTILES;
+        const bool small = vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= kSmallMaxQtiles;
         if (small && fa_f32_padded_dim(a.D) == 32) {
             if (probs)
-                return causal ? fa::launch_fa<TS, NQ, NK, 1, true, true, true, ST>(a, stream)
-                              : fa::launch_fa<TS, NQ, NK, 1, false, true, true, ST>(a, stream);
-            return causal ? fa::launch_fa<TS, NQ, NK, 1, true, false, true>(a, stream)
-                          : fa::launch_fa<TS, NQ, NK, 1, false, false, true>(a, stream);
+                return causal ? fa::launch_fa<TS, NQ, NK, true, true, true, ST>(a, stream)
+                              : fa::launch_fa<TS, NQ, NK, false, true, true, ST>(a, stream);
+            return causal ? fa::launch_fa<TS, NQ, NK, true, false, true>(a, stream)
+                          : fa::launch_fa<TS, NQ, NK, false, false, true>(a, stream);
         }
-#if HIPGPT_F32_SMALL64
         using T6 = F32Traits<64, true, ST>;
-        if (vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= HIPGPT_F32_SMALL64_MAX_QTILES &&
-            fa_f32_padded_dim(a.D) == 64) {
+        if (vec && a.Sk >= 128 && a.Sk <= 256 && qtiles <= kSmall64MaxQtiles && fa_f32_padded_dim(a.D) == 64) {
             if (probs)
-                return causal ? fa::launch_fa<T6, NQ, NK, 1, true, true, true, ST>(a, stream)
-                              : fa::launch_fa<T6, NQ, NK, 1, false, true, true, ST>(a, stream);
-            return causal ? fa::launch_fa<T6, NQ, NK, 1, true, false, true>(a, stream)
-                          : fa::launch_fa<T6, NQ, NK, 1, false, false, true>(a, stream);
+                return causal ? fa::launch_fa<T6, NQ, NK, true, true, true, ST>(a, stream)
+                              : fa::launch_fa<T6, NQ, NK, false, true, true, ST>(a, stream);
+            return causal ? fa::launch_fa<T6, NQ, NK, true, false, true>(a, stream)
+                          : fa::launch_fa<T6, NQ, NK, false, false, true>(a, stream);
         }
-#endif
     }
-#endif
-    if (vec && a.Sq <= HIPGPT_RESIDENT_MAX_SQ && !a.lse) {  // the resident kernel writes no lse
-#if HIPGPT_RES_D32_NKS > 0
-        if (a.D == 32 && fa::resident_lds_bytes<F32Traits<32>, 8, HIPGPT_RES_D32_NKS>(a) != 0)
-            return fa::launch_resident<F32Traits<32>, 8, HIPGPT_RES_D32_NKS, 4>(a, causal, stream);
-#endif
-        // one workgroup per (b, h) and CU: only when the (b, h) pairs fill
-        // the device (at B*H = 128, S = 256 the streaming kernel measured
-        // 38.8 against 53.7 us for the drop-in, 24.3 against 31.2 causal)
-        if (a.D == 64 && (int64_t)a.B * a.H >= device_cus() &&
-            fa::resident_lds_bytes<F32Traits<64, true>, 8, 1>(a) != 0)
-            return fa::launch_resident<F32Traits<64, true>, 8, 1, 4>(a, causal, stream);
-    }
+    // one workgroup per (b, h) and CU: only when the (b, h) pairs fill the
+    // device (at B*H = 128, S = 256 the streaming kernel measured 38.8 against
+    // 53.7 us for the drop-in, 24.3 against 31.2 causal); the resident kernel
+    // writes no lse
+    if (vec && a.Sq <= kResidentMaxSq && !a.lse && a.D == 64 && (int64_t)a.B * a.H >= device_cus() &&
+        fa::resident_lds_bytes<F32Traits<64, true>, 8>(a) != 0)
+        return fa::launch_resident<F32Traits<64, true>, 8, 4>(a, causal, stream);
     switch (fa_f32_padded_dim(a.D)) {
-        case 32:
-            return launch_dp<32, HIPGPT_F32_D32_NQS, HIPGPT_F32_D32_NKS, HIPGPT_F32_D32_PF>(a, causal, probs, vec, stream);
-        case 64:
-            return launch_dp<64, HIPGPT_F32_D64_NQS, HIPGPT_F32_D64_NKS, HIPGPT_F32_D64_PF>(a, causal, probs, vec, stream);
-        case 128:
-            return launch_dp<128, HIPGPT_F32_D128_NQS, HIPGPT_F32_D128_NKS, HIPGPT_F32_D128_PF>(a, causal, probs, vec,
-                                                                                         stream);
+        case 32: return launch_dp<32, 2, 2>(a, causal, probs, vec, stream);
+        case 64: return launch_dp<64, 4, 2>(a, causal, probs, vec, stream);
+        case 128: return launch_dp<128, 8, 1>(a, causal, probs, vec, stream);
         default: return hipErrorInvalidValue;
     }
 }

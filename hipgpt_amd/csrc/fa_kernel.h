@@ -36,42 +36,29 @@ namespace fa {
 // at least half of the device's workgroup slots (c1: 16.1 -> 15.8 us against 200 ns;
 // measured over 100 .. 800 ns per rank; re-measured on cache-rotated inputs
 // at 250 .. 550 ns: within 0.1 us rotated, 350 ns best hot).
-#ifndef HIPGPT_FA_STAGGER_TICKS
-#define HIPGPT_FA_STAGGER_TICKS 35
-#endif
-constexpr unsigned long long kStaggerTicks = HIPGPT_FA_STAGGER_TICKS;
+constexpr unsigned long long kStaggerTicks = 35;
 // The same for grids that write probs: 1 us per rank without a causal mask
 // (c1 drop-in 31.3 -> 29.9 us), 700 ns with one (c1 with probs 25.0 ->
 // 24.7 us); measured over 0.4 .. 1.6 us per rank.
 constexpr unsigned long long kStaggerTicksProbs = 100;
 constexpr unsigned long long kStaggerTicksProbsCausal = 70;
-// Score-resident probs sweep: probs tiles stored through an LDS transpose as
-// whole 128-byte rows (1), non-temporal (2), or straight from the
-// accumulator layout, 32 bytes per row per instruction (0).  Measured
-// (cache-rotated / hot, us): c1 with probs 31.2 / 24.5 -> 28.6 / 24.6, the c1
-// drop-in 34.9 / 29.6 -> 33.1 / 30.0, B = 128 drop-in 138.7 / 124.2 ->
-// 124.7 / 111.2 with 2; 1 alone gained less rotated and lost hot.
-#ifndef HIPGPT_PROBS_TRANSPOSE
-#define HIPGPT_PROBS_TRANSPOSE 2
-#endif
-// O stores of the streaming kernel through a per-wave LDS transpose, as whole
-// rows of the head: plain (1) or non-temporal (2).  With 2, c1 17.85 -> 16.84 us
-// (cache-rotated; hot 15.77 -> 14.95), the c1 drop-in 33.2 -> 31.4 us; 1 alone
-// measured level, and non-temporal stores of the accumulator layout's 32-byte
-// row pieces were slower (c1 17.6 us).
-#ifndef HIPGPT_O_TRANSPOSE
-#define HIPGPT_O_TRANSPOSE 2
-#endif
-#ifndef HIPGPT_PROBS_TRANSPOSE_MIN_DP
-#define HIPGPT_PROBS_TRANSPOSE_MIN_DP 128
-#endif
-#ifndef HIPGPT_SPILL_NT
-#define HIPGPT_SPILL_NT 1
-#endif
-#ifndef HIPGPT_FA_STAGGER_MAX_BLOCKS
-#define HIPGPT_FA_STAGGER_MAX_BLOCKS 4
-#endif
-constexpr int kStaggerMaxBlocks = HIPGPT_FA_STAGGER_MAX_BLOCKS;  // 0: no start stagger
+// Probs tiles of the score-resident sweep, and of the causal probs sweeps at
+// padded head dims >= kTransOwnMinDP (one workgroup per CU, LDS to spare),
+// are stored through a per-wave LDS transpose as whole 128-byte rows,
+// non-temporally, instead of straight from the accumulator layout (32 bytes
+// per row per instruction).  Measured (cache-rotated / hot, us): c1 with probs
+// 31.2 / 24.5 -> 28.6 / 24.6, the c1 drop-in 34.9 / 29.6 -> 33.1 / 30.0,
+// B = 128 drop-in 138.7 / 124.2 -> 124.7 / 111.2; plain (not non-temporal)
+// whole-row stores gained less rotated and lost hot.  The spilled scores of
+// those causal sweeps leave the same way.
+constexpr int kTransOwnMinDP = 128;
+// O stores of the streaming kernel go through a per-wave LDS transpose as
+// whole rows of the head, non-temporally: c1 17.85 -> 16.84 us (cache-rotated;
+// hot 15.77 -> 14.95), the c1 drop-in 33.2 -> 31.4 us; the transpose with
+// plain stores measured level, and non-temporal stores of the accumulator
+// layout's 32-byte row pieces were slower (c1 17.6 us).
+// Start stagger only for grids of at most this many query blocks per (b, h).
+constexpr int kStaggerMaxBlocks = 4;
 
 // SRT > 0 (probs only): when a wave's key tiles span at most SRT stages, the
 // max/sum sweep keeps every score tile in registers and the probs sweep reads
@@ -87,9 +74,8 @@ constexpr int kStaggerMaxBlocks = HIPGPT_FA_STAGGER_MAX_BLOCKS;  // 0: no start 
 // sweep iteration ends with a workgroup barrier (and one precedes the first
 // read-back prefetch), which orders each global store before the loads of the
 // other lanes.  A change that removes those barriers breaks the spill.
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
+template <class TR, int NQS, int NKS, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 struct FaKernel {
-    static_assert(PF == 1 || PF == 2, "prefetch depth is one or two stages");
     static constexpr int DP = TR::DP;
     static constexpr int NW = NQS * NKS;
     static constexpr int NT = NW * 64;
@@ -105,15 +91,13 @@ struct FaKernel {
     static constexpr int BASE_BYTES = (2 * STAGE_BYTES > MERGE_BYTES) ? 2 * STAGE_BYTES : MERGE_BYTES;
     // Probs stores through a per-wave LDS transpose (see store_t): the score-
     // resident sweep borrows the idle K half of the stage buffers; the causal
-    // probs sweeps at padded D >= HIPGPT_PROBS_TRANSPOSE_MIN_DP (one workgroup
+    // probs sweeps at padded D >= kTransOwnMinDP (one workgroup
     // per CU, LDS to spare) get a region of their own after BASE_BYTES, for
     // the spilled scores and the probs alike (B4 H16 S2048 D128 with probs
     // 880 -> 867 us).  Unmasked there, the transpose measured slower (the
     // drop-in 1391 -> 1465 us).
-    static constexpr bool TRANS_RES = HIPGPT_PROBS_TRANSPOSE && SRT > 0 && sizeof(E) == 4 &&
-                                      TR::KTILE >= QW * 36 && NW <= 2 * NKS;
-    static constexpr bool TRANS_OWN = HIPGPT_PROBS_TRANSPOSE && PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 &&
-                                      DP >= HIPGPT_PROBS_TRANSPOSE_MIN_DP;
+    static constexpr bool TRANS_RES = SRT > 0 && sizeof(E) == 4 && TR::KTILE >= QW * 36 && NW <= 2 * NKS;
+    static constexpr bool TRANS_OWN = PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 && DP >= kTransOwnMinDP;
     static constexpr int LDS_BYTES = BASE_BYTES + (TRANS_OWN ? NW * QW * 36 * 4 : 0);
     // O stores through LDS, one 32-dim block at a time (whole 128-byte row
     // segments per lane group), with a 32 x 36 scratch per storing wave
@@ -121,7 +105,7 @@ struct FaKernel {
     // fits there, else over it after a barrier.  Only with 16-byte rows of the
     // full padded head (VEC, D = DP).
     static constexpr int O_SCR = NQS * QW * 36 * 4;
-    static constexpr bool O_TRANS = HIPGPT_O_TRANSPOSE && VEC && O_SCR <= BASE_BYTES;
+    static constexpr bool O_TRANS = VEC && O_SCR <= BASE_BYTES;
     static constexpr bool O_TRANS_PAST = MERGE_BYTES + O_SCR <= BASE_BYTES;
 
     // Global -> register staging of one stage (K and V), 16-byte chunks.
@@ -136,7 +120,7 @@ struct FaKernel {
     // problems -- D below the padded dim or unaligned strides -- use plain
     // guarded loads.)
     struct Stager {
-        typename TR::chunk kr[PF][PER], vr[PF][PER];  // PF register slots of one stage each
+        typename TR::chunk kr[PER], vr[PER];  // one stage of K and V chunks
         int koff[PER], voff[PER];  // byte offsets of this thread's chunks from the stage's first row
         __amdgpu_buffer_rsrc_t krs, vrs;
         int kstage, vstage;        // bytes per stage of NKS*BK rows
@@ -171,7 +155,7 @@ struct FaKernel {
             }
         }
 
-        template <int SL, bool WV = true, bool WK = true>
+        template <bool WV = true, bool WK = true>
         __device__ __forceinline__ void load(int stage, int tid) {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -179,21 +163,21 @@ struct FaKernel {
                 if (VEC) {
                     if (CPS % NT == 0 || f < CPS) {
                         if (WK)
-                            kr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
+                            kr[i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(krs, koff[i] + stage * kstage, 0, 0));
                         if (WV)
-                            vr[SL][i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
+                            vr[i] = TR::from_u32x4(__builtin_amdgcn_raw_buffer_load_b128(vrs, voff[i] + stage * vstage, 0, 0));
                     }
                 } else {
                     const int row = f / CPR;  // 0 .. NKS*BK-1
                     const int cc = f % CPR;
                     const int key = stage * NKS * BK + row;
                     const bool ok = (CPS % NT == 0 || f < CPS) && key < Sk;
-                    if (WK) kr[SL][i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
-                    if (WV) vr[SL][i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
+                    if (WK) kr[i] = TR::template load_chunk<false>(Kp, (int64_t)key * kts, cc, D, ok);
+                    if (WV) vr[i] = TR::template load_chunk<false>(Vp, (int64_t)key * vts, cc, D, ok);
                 }
             }
         }
-        template <int SL, bool WV = true, bool WK = true>
+        template <bool WV = true, bool WK = true>
         __device__ __forceinline__ void store(E* stage, int tid) const {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -205,8 +189,8 @@ struct FaKernel {
                 const int r = row % BK;
                 E* Kt = stage + kt * TR::KTILE;
                 E* Vt = stage + NKS * TR::KTILE + kt * TR::VTILE;
-                if (WK) TR::store_k_chunk(Kt, r, cc, kr[SL][i]);
-                if (WV) TR::store_vt_chunk(Vt, r, cc, vr[SL][i]);
+                if (WK) TR::store_k_chunk(Kt, r, cc, kr[i]);
+                if (WV) TR::store_vt_chunk(Vt, r, cc, vr[i]);
             }
         }
     };
@@ -324,10 +308,10 @@ struct FaKernel {
         // Probs stores through LDS: the wave writes its tile ([query][key], 16
         // keys per lane in the accumulator layout) into a private 32 x 36
         // scratch X and reads it back as 8 whole 128-byte rows per
-        // instruction, so every store writes full lines (optionally
-        // non-temporal).  X is the wave's own: a memory clobber orders the
+        // instruction, so every store writes full lines, non-temporally.  X is
+        // the wave's own: a memory clobber orders the
         // exchange between its lanes.  prow0: row qw0 of the probs.
-        auto store_t = [&](float* X, float* prow0, const floatx16& p, int tb, bool pvec, bool nt) {
+        auto store_t = [&](float* X, float* prow0, const floatx16& p, int tb, bool pvec) {
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 *reinterpret_cast<floatx4*>(X + c * 36 + 8 * g + 4 * hf) =
@@ -342,10 +326,7 @@ struct FaKernel {
                 if (qw0 + row < Sq) {
                     float* dst = prow0 + (int64_t)row * Sk + tb + cc;
                     if (full) {
-                        if (nt)
-                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
-                        else
-                            *reinterpret_cast<floatx4*>(dst) = v;
+                        __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
                     } else {
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
@@ -400,7 +381,7 @@ struct FaKernel {
                 TR::pv(vreg, s, o, c, hf);
             } else if (MODE == 1) {
                 if constexpr (SPILL && TRANS_OWN)
-                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec, HIPGPT_SPILL_NT);
+                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec);
                 else if (SPILL && qi < Sq)
                     store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 const float m_new = vmax(m_run, tile_max(s) * sc);
@@ -413,38 +394,30 @@ struct FaKernel {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], sc, -mlog));
                 if constexpr (TRANS_OWN)
-                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec, HIPGPT_PROBS_TRANSPOSE > 1);
+                    store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec);
                 else if (qi < Sq)
                     store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 TR::pv(vreg, s, o, c, hf);
             }
         };
 
-        // Stage pipeline.  PF = 1: stage i+1 is loaded into registers while
-        // stage i is computed.  PF = 2: two register slots; stage i+2 is
-        // requested while stage i is computed and stage i+1 (requested one
-        // stage earlier) is written to LDS afterwards, so every global load
-        // has two stages of compute to land.
+        // Stage pipeline: stage i+1 is loaded into registers while stage i is
+        // computed, then written to the other LDS buffer.  (Two stages of
+        // register prefetch measured no faster at any head dim and cost an
+        // occupancy step at D = 32.)
         auto sweep = [&](auto mode_tag, float mlog, float* prow, bool pvec) {
             constexpr bool WV = decltype(mode_tag)::value != 1;  // the max/sum sweep stages no V
             constexpr bool WK = !(SPILL && decltype(mode_tag)::value == 2);  // nor the spilled probs sweep K
             if (nstages > 0) {
-                st.template load<0, WV, WK>(0, tid);
-                if (PF == 2 && nstages > 1) st.template load<PF - 1, WV, WK>(1, tid);
-                st.template store<0, WV, WK>(lds, tid);
+                st.template load<WV, WK>(0, tid);
+                st.template store<WV, WK>(lds, tid);
             }
             __syncthreads();
-            auto iter = [&](int i, auto slot_tag) {
-                constexpr int SL = decltype(slot_tag)::value;  // slot free for new loads
-                constexpr int NX = PF == 2 ? 1 - SL : 0;      // slot holding stage i+1
-                if (i + PF < nstages) st.template load<SL, WV, WK>(i + PF, tid);
+            for (int i = 0; i < nstages; ++i) {
+                if (i + 1 < nstages) st.template load<WV, WK>(i + 1, tid);
                 compute(mode_tag, i, mlog, prow, pvec);
-                if (i + 1 < nstages) st.template store<NX, WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                if (i + 1 < nstages) st.template store<WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
                 __syncthreads();
-            };
-            for (int i = 0; i < nstages; i += PF) {
-                iter(i, std::integral_constant<int, 0>{});
-                if (PF == 2 && i + 1 < nstages) iter(i + 1, std::integral_constant<int, PF - 1>{});
             }
         };
 
@@ -454,15 +427,15 @@ struct FaKernel {
         auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
             if (nstages > 0) {
-                st.template load<0, SECOND, !SECOND>(0, tid);
-                st.template store<0, SECOND, !SECOND>(lds, tid);
+                st.template load<SECOND, !SECOND>(0, tid);
+                st.template store<SECOND, !SECOND>(lds, tid);
             }
             __syncthreads();
             static_for(
                 [&](auto ic) {
                     constexpr int I = decltype(ic)::value;
                     if (I < nstages) {
-                        if (I + 1 < nstages) st.template load<0, SECOND, !SECOND>(I + 1, tid);
+                        if (I + 1 < nstages) st.template load<SECOND, !SECOND>(I + 1, tid);
                         const E* cur = lds + (I & 1) * STAGE_ELEMS;
                         const int t = I * NKS + ks;
                         if (t < wtiles) {
@@ -484,7 +457,7 @@ struct FaKernel {
                                 if constexpr (TRANS_RES) {
                                     float* const X = reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS +
                                                                               (wave % NKS) * TR::KTILE);
-                                    store_t(X, prow - (int64_t)c * Sk, p, t * BK, pvec, HIPGPT_PROBS_TRANSPOSE > 1);
+                                    store_t(X, prow - (int64_t)c * Sk, p, t * BK, pvec);
                                 } else {
                                     if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
                                 }
@@ -492,7 +465,7 @@ struct FaKernel {
                             }
                         }
                         if (I + 1 < nstages)
-                            st.template store<0, SECOND, !SECOND>(lds + ((I + 1) & 1) * STAGE_ELEMS, tid);
+                            st.template store<SECOND, !SECOND>(lds + ((I + 1) & 1) * STAGE_ELEMS, tid);
                         __syncthreads();
                     }
                 },
@@ -551,14 +524,13 @@ struct FaKernel {
                 }
             }
         } else {
-#if HIPGPT_ZERO_FIRST
             // Causal: the zeros above the diagonal need no data, so they are
-            // stored before the sweeps, while the first stage's loads are in flight.
+            // stored before the sweeps, while the first stage's loads are in
+            // flight (c1 with probs 26.5 -> 25.2 us against storing them last).
             if (CAUSAL && qw0 < Sq && ks == 0) {
                 const bool pv0 = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
                 zero_probs_tail<(SRT > 0)>(a.probs + (int64_t)bh * Sq * Sk, qw0, Sq, Sk, tr.wtiles * BK, lane, pv0);
             }
-#endif
             float* probs_bh = a.probs + (int64_t)bh * Sq * Sk;
             const bool pvec = (Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0;
             if constexpr (SRT > 0)
@@ -590,10 +562,6 @@ struct FaKernel {
                 sweep_res(std::true_type{}, mlog, probs_bh + (int64_t)qi * Sk, pvec);
             else
                 sweep(std::integral_constant<int, 2>{}, mlog, probs_bh + (int64_t)qi * Sk, pvec);
-            if (!HIPGPT_ZERO_FIRST && CAUSAL && qw0 < Sq && ks == 0) {
-                const int ztile = tr.wtiles;  // tiles [0, wtiles) were written by the NKS waves
-                zero_probs_tail(probs_bh, qw0, Sq, Sk, ztile * BK, lane, pvec);
-            }
             if (NKS > 1) {
                 if (ks != 0) {
                     // (scalar slots here: 16-byte ones spill the D = 64 probs kernel under its 128-register cap)
@@ -643,10 +611,7 @@ struct FaKernel {
                         const floatx4 v = *reinterpret_cast<const floatx4*>(X + row * 36 + cc);
                         if (qw0 + row < Sq) {
                             float* dst = o0 + (int64_t)row * a.o_ts + db * 32 + cc;
-                            if (HIPGPT_O_TRANSPOSE > 1)
-                                __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
-                            else
-                                *reinterpret_cast<floatx4*>(dst) = v;
+                            __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst));
                         }
                     }
                     asm volatile("" ::: "memory");  // the next block's writes come after these reads
@@ -684,22 +649,22 @@ struct waves_per_eu { static constexpr int value = 1; };
 template <class TR>
 struct waves_per_eu<TR, std::void_t<decltype(TR::WAVES_PER_EU)>> { static constexpr int value = TR::WAVES_PER_EU; };
 
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
+template <class TR, int NQS, int NKS, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 __global__ __launch_bounds__(NQS* NKS * 64) __attribute__((amdgpu_waves_per_eu(VEC ? waves_per_eu<TR>::value : 1)))
 void fa_fwd_kernel(AttnArgs a) {
-    using K = FaKernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>;
+    using K = FaKernel<TR, NQS, NKS, CAUSAL, PROBS, VEC, SRT>;
     __shared__ __attribute__((aligned(16))) unsigned char lds[K::LDS_BYTES];
     __shared__ int simd_slots[NQS * NKS];
     K::run(a, lds, simd_slots);
 }
 
-template <class TR, int NQS, int NKS, int PF, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
+template <class TR, int NQS, int NKS, bool CAUSAL, bool PROBS, bool VEC, int SRT = 0>
 hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     AttnArgs args = a;
     args.n_qblk = (a.Sq + NQS * QW - 1) / (NQS * QW);
     const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    auto kern = fa_fwd_kernel<TR, NQS, NKS, PF, CAUSAL, PROBS, VEC, SRT>;
+    auto kern = fa_fwd_kernel<TR, NQS, NKS, CAUSAL, PROBS, VEC, SRT>;
     args.stagger_slots = 0;
     if ((CAUSAL || PROBS) && args.n_qblk > 1 && args.n_qblk <= kStaggerMaxBlocks) {
         static ResidentSlots cache;
@@ -719,12 +684,7 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
 // operands at D = 128 (B4 H16 S2048: 1623 -> 1504 us for the drop-in
 // launcher) and slower at D = 64 (B8 H12 S1024: 327 -> 388 us), so it is
 // used for fp32 operands with a padded head size of 128 or more.
-#ifndef HIPGPT_SCORE_SPILL
-#define HIPGPT_SCORE_SPILL 1
-#endif
-#ifndef HIPGPT_SCORE_SPILL_MIN_DP
-#define HIPGPT_SCORE_SPILL_MIN_DP 128
-#endif
+constexpr int kScoreSpillMinDP = 128;
 
 // Score-resident stages of a traits type (PROBS_RES_STAGES; 0 = the probs
 // sweeps recompute Q K^T).
@@ -735,28 +695,28 @@ struct probs_res_stages<TR, std::void_t<decltype(TR::PROBS_RES_STAGES)>> {
     static constexpr int value = TR::PROBS_RES_STAGES;
 };
 
-template <class TR, int NQS, int NKS, int PF, bool VEC>
+template <class TR, int NQS, int NKS, bool VEC>
 hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
     constexpr int SRT = probs_res_stages<TR>::value;
-    constexpr bool kSpill = HIPGPT_SCORE_SPILL && VEC && sizeof(typename TR::elem) == 4 && TR::DP >= HIPGPT_SCORE_SPILL_MIN_DP;
+    constexpr bool kSpill = VEC && sizeof(typename TR::elem) == 4 && TR::DP >= kScoreSpillMinDP;
     if constexpr (SRT > 0) {
         // every wave's key tiles fit the resident stages (Sk <= SRT * NKS * 32)
         if (probs && ((a.Sk + BK - 1) / BK + NKS - 1) / NKS <= SRT)
-            return causal ? launch_fa<TR, NQS, NKS, PF, true, true, VEC, SRT>(a, s)
-                          : launch_fa<TR, NQS, NKS, PF, false, true, VEC, SRT>(a, s);
+            return causal ? launch_fa<TR, NQS, NKS, true, true, VEC, SRT>(a, s)
+                          : launch_fa<TR, NQS, NKS, false, true, VEC, SRT>(a, s);
     }
     // longer rows: the scores are spilled to the probs buffer between the
     // sweeps (16-byte aligned probs rows)
     if constexpr (kSpill) {
         if (probs && (a.Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0)
-            return causal ? launch_fa<TR, NQS, NKS, PF, true, true, VEC, -1>(a, s)
-                          : launch_fa<TR, NQS, NKS, PF, false, true, VEC, -1>(a, s);
+            return causal ? launch_fa<TR, NQS, NKS, true, true, VEC, -1>(a, s)
+                          : launch_fa<TR, NQS, NKS, false, true, VEC, -1>(a, s);
     }
     if (causal)
-        return probs ? launch_fa<TR, NQS, NKS, PF, true, true, VEC>(a, s)
-                     : launch_fa<TR, NQS, NKS, PF, true, false, VEC>(a, s);
-    return probs ? launch_fa<TR, NQS, NKS, PF, false, true, VEC>(a, s)
-                 : launch_fa<TR, NQS, NKS, PF, false, false, VEC>(a, s);
+        return probs ? launch_fa<TR, NQS, NKS, true, true, VEC>(a, s)
+                     : launch_fa<TR, NQS, NKS, true, false, VEC>(a, s);
+    return probs ? launch_fa<TR, NQS, NKS, false, true, VEC>(a, s)
+                 : launch_fa<TR, NQS, NKS, false, false, VEC>(a, s);
 }
 
 }  // namespace fa

@@ -4,7 +4,7 @@
 // At S = 256 the streaming kernel (fa_kernel.h) spends a large share of its
 // time in the prologue (every workgroup loads Q and its first stage at once)
 // and in per-stage barriers that keep waves with unequal causal work in
-// lockstep.  Here one workgroup of NQS x NKS waves owns NQS*32 queries of one
+// lockstep.  Here one workgroup of NQS = 8 waves owns 256 queries of one
 // (b, h) and keeps every K tile (row-major) and V^T tile it needs in LDS:
 //   * Production: tile t is split over all threads; each thread keeps L
 //     tiles of loads in flight in registers, writes its share of tile t to
@@ -15,14 +15,14 @@
 //     workgroup barrier after the first, so waves with little causal work
 //     finish early instead of idling in lockstep.
 //   * Balance: the waves are ranked by the SIMD the hardware placed them on
-//     (simd_rank).  With NW/4 waves per SIMD, the waves of SIMD s take query
-//     sub-blocks s and NQS-1-s (NQS = 8), and with NKS = 2 each sub-block's
-//     tiles alternate between two waves, so every SIMD carries the same
-//     causal work; the NKS partial (m, l, O) are merged in LDS at the end.
-//   * With probs the second sweep re-reads K/V from LDS (no reload).  With
-//     one key split and at most 8 tiles (D = 64: the LDS holds no more), each
-//     wave keeps its masked score tiles in registers between the sweeps, so
-//     the probs sweep runs P V only instead of recomputing Q K^T.
+//     (simd_rank).  With two waves per SIMD, the waves of SIMD s take query
+//     sub-blocks s and 7-s, so every SIMD carries the same causal work.
+//   * With probs the second sweep re-reads K/V from LDS (no reload).  With at
+//     most 8 tiles (D = 64: the LDS holds no more), each wave keeps its masked
+//     score tiles in registers between the sweeps, so the probs sweep runs
+//     P V only instead of recomputing Q K^T.
+// (A variant with each sub-block's key tiles split over two waves, for
+// D = 32, measured slower than the streaming kernel there and was removed.)
 // The per-tile math (S^T = K Q^T, mask, online softmax, O^T += V^T P^T) is the
 // same as the streaming kernel's, through the same operand traits.
 #pragma once
@@ -41,18 +41,11 @@ namespace fa {
 // SIMD ranking, sits in the rest of the 160 KB).
 constexpr int kResidentLdsMax = 152 * 1024;
 constexpr int kResidentLdsLimit = 160 * 1024 - 256;
-#ifndef HIPGPT_RES_O_TRANSPOSE
-#define HIPGPT_RES_O_TRANSPOSE 1
-#endif
 
-#ifndef HIPGPT_RES_SCORES
-#define HIPGPT_RES_SCORES 1
-#endif
-
-template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
+template <class TR, int NQS, int L, bool CAUSAL, bool PROBS>
 struct FaResident {
-    static_assert(NQS == 8 && (NKS == 1 || NKS == 2), "8 sub-blocks, one or two key splits");
-    static constexpr int NW = NQS * NKS;
+    static_assert(NQS == 8, "8 sub-blocks, two waves per SIMD");
+    static constexpr int NW = NQS;
     static constexpr int DP = TR::DP;
     static constexpr int NT = NW * 64;
     static constexpr int NDB = DP / 32;
@@ -64,21 +57,17 @@ struct FaResident {
     static constexpr int PER = (2 * CPT + NT - 1) / NT;  // K+V chunks per thread per tile
     static_assert(CPT % 64 == 0, "a wave's chunks are all K or all V");
 
-    // LDS layout: [0, 256) arrival counters; [256, 256 + ML_BYTES) per-wave
-    // (m, l) for the probs sweep merge; then the tiles.  The final O merge
-    // reuses the tile area (after a barrier).
-    static constexpr int ML_BYTES = NKS > 1 ? NW * 64 * 2 * 4 : 0;
-    static constexpr int HEAD_BYTES = 256 + ML_BYTES;
-    static constexpr int MERGE_BYTES = NKS > 1 ? NW * 64 * 16 * NDB * 4 : 0;
+    // LDS layout: [0, 256) arrival counters, then the tiles.
+    static constexpr int HEAD_BYTES = 256;
     // Score tiles kept in registers between the probs sweeps (0: recomputed).
     // The LDS bounds a wave's tiles: ceil(Sk / 32) <= MAX_TILES.
     static constexpr int MAX_TILES = kResidentLdsMax / (TILE_ELEMS * (int)sizeof(E));
-    static constexpr int SRES = (HIPGPT_RES_SCORES && PROBS && NKS == 1 && MAX_TILES <= 8) ? MAX_TILES : 0;
+    static constexpr int SRES = (PROBS && MAX_TILES <= 8) ? MAX_TILES : 0;
     // O stores through a per-wave 16 x 36 scratch past the tiles (whole
     // 128-byte row segments, non-temporal): c2 33.9 -> 32.8 us.  Not with
     // probs, where the larger LDS footprint measured slower (c2 with probs
     // 41.3 -> 48.6 us, drop-in 56.1 -> 60.3 us).
-    static constexpr bool O_TRANS = HIPGPT_RES_O_TRANSPOSE && !PROBS && sizeof(E) == 4;
+    static constexpr bool O_TRANS = !PROBS && sizeof(E) == 4;
     static constexpr int O_TRANS_BYTES = O_TRANS ? NW * 16 * 36 * 4 : 0;
 
     __device__ __forceinline__ static void run(const AttnArgs& a, unsigned char* lds_raw, int ntiles_max,
@@ -98,14 +87,12 @@ struct FaResident {
         const int qb = CAUSAL ? a.n_qblk - 1 - rank : rank;
         const int b = bh / a.H;
         const int h = bh % a.H;
-        // Ranked by SIMD, waves 4j .. 4j+3 of the ranking sit on SIMD j when the
-        // hardware puts NW/4 waves on each SIMD: the waves of a SIMD take
-        // sub-blocks s and NQS-1-s, key splits 0 and 1.
+        // Ranked by SIMD, waves 2j and 2j+1 of the ranking sit on SIMD j when
+        // the hardware puts two waves on each SIMD: they take sub-blocks j and
+        // NQS-1-j.
         const int rk = simd_rank<NW>(simd_slots, wave, lane);
-        const int simd = rk / (NW / 4), grp = rk % (NW / 4);
-        const int sub = (grp & 1) ? NQS - 1 - simd : simd;
-        const int ks = grp >> 1;
-        const int slot = sub * NKS + ks;
+        const int simd = rk / 2;
+        const int sub = (rk & 1) ? NQS - 1 - simd : simd;
 
         const int q0 = qb * (NQS * QW);
         const int qw0 = q0 + sub * QW;
@@ -262,7 +249,7 @@ struct FaResident {
                 publish(t + L, slot_tag);
                 if (t + 2 * L < T) issue(t + 2 * L, slot_tag);
             }
-            if (t < wtiles && t % NKS == ks) {
+            if (t < wtiles) {
                 wait_tile(t);
                 consume(t);
             }
@@ -305,21 +292,7 @@ struct FaResident {
         }
 
         if (!PROBS) l_run = halves_sum(l_run);
-        float* const ml = reinterpret_cast<float*>(lds_raw + 256);  // [NW][2][64]
         if (PROBS) {
-            if (NKS > 1) {  // combine the splits' (m, l): every split needs the row's final values
-                ml[(slot * 2) * 64 + lane] = m_run;
-                ml[(slot * 2 + 1) * 64 + lane] = l_run;
-                __syncthreads();
-                float M = kMaxInit, L2 = 0.f;
-#pragma unroll
-                for (int j = 0; j < NKS; ++j) M = fmaxf(M, ml[((sub * NKS + j) * 2) * 64 + lane]);
-#pragma unroll
-                for (int j = 0; j < NKS; ++j)
-                    L2 = fmaf(ml[((sub * NKS + j) * 2 + 1) * 64 + lane], fast_exp2(ml[((sub * NKS + j) * 2) * 64 + lane] - M), L2);
-                m_run = M;
-                l_run = L2;
-            }
             // sweep 2 from the resident tiles: P = exp(s - m) / l stored once, P V
             // P = exp2(s' - (m + log2 l)): the normalisation rides in the exponent
             const float mlog = m_run + __builtin_amdgcn_logf(fmaxf(l_run, 1e-20f));
@@ -342,64 +315,18 @@ struct FaResident {
                     },
                     std::make_integer_sequence<int, (SRES > 0 ? SRES : 1)>{});
             } else {
-                for (int t = ks; t < wtiles; t += NKS) probs_tile(t, scores(t));
+                for (int t = 0; t < wtiles; ++t) probs_tile(t, scores(t));
             }
-            if (CAUSAL && qw0 < Sq && ks == 0) zero_probs_tail(probs_bh, qw0, Sq, Sk, wtiles * BK, lane, pvec);
+            if (CAUSAL && qw0 < Sq) zero_probs_tail(probs_bh, qw0, Sq, Sk, wtiles * BK, lane, pvec);
             l_run = 1.0f;
-        }
-
-        if (NKS > 1) {
-            // merge the key splits of each sub-block through the (now idle) tile area
-            float* const mo = reinterpret_cast<float*>(tiles);  // [NW][16*NDB][64]
-            __syncthreads();
-            if (ks != 0) {
-                ml[(slot * 2) * 64 + lane] = m_run;
-                ml[(slot * 2 + 1) * 64 + lane] = l_run;
-#pragma unroll
-                for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) mo[(slot * 16 * NDB + db * 16 + r) * 64 + lane] = o[db][r];
-            }
-            __syncthreads();
-            if (ks == 0) {
-                if (PROBS) {  // partial O are already normalised: sum them
-#pragma unroll
-                    for (int j = 1; j < NKS; ++j)
-#pragma unroll
-                        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) o[db][r] += mo[((slot + j) * 16 * NDB + db * 16 + r) * 64 + lane];
-                } else {
-                    float M = m_run;
-#pragma unroll
-                    for (int j = 1; j < NKS; ++j) M = fmaxf(M, ml[((slot + j) * 2) * 64 + lane]);
-                    const float w0 = fast_exp2(m_run - M);
-                    l_run *= w0;
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) o[db][r] *= w0;
-#pragma unroll
-                    for (int j = 1; j < NKS; ++j) {
-                        const float wj = fast_exp2(ml[((slot + j) * 2) * 64 + lane] - M);
-                        l_run = fmaf(ml[((slot + j) * 2 + 1) * 64 + lane], wj, l_run);
-#pragma unroll
-                        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                o[db][r] = fmaf(mo[((slot + j) * 16 * NDB + db * 16 + r) * 64 + lane], wj, o[db][r]);
-                    }
-                }
-            }
         }
 
         if constexpr (O_TRANS) {
             // O through the wave's 16 x 36 scratch past the tiles, one 32-dim
             // block and 16 query rows at a time: whole 128-byte row segments
             // per lane group, non-temporal
-            if (ks == 0) {
-                int body = ntiles_max * TILE_ELEMS * (int)sizeof(E);
-                if (body < MERGE_BYTES) body = MERGE_BYTES;
+            {
+                const int body = ntiles_max * TILE_ELEMS * (int)sizeof(E);
                 float* const X = reinterpret_cast<float*>(lds_raw + HEAD_BYTES + body) + wave * 16 * 36;
                 const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
                 float* const o0 = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qw0 * a.o_ts;
@@ -426,7 +353,7 @@ struct FaResident {
                         asm volatile("" ::: "memory");  // the next pass's writes come after these reads
                     }
             }
-        } else if (ks == 0 && qi < Sq) {
+        } else if (qi < Sq) {
             const float linv = __builtin_amdgcn_rcpf(fmaxf(l_run, 1e-20f));
             float* orow = a.o + b * a.o_bs + h * a.o_hs + (int64_t)qi * a.o_ts;
 #pragma unroll
@@ -440,30 +367,29 @@ struct FaResident {
     }
 };
 
-template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
-__global__ __launch_bounds__(NQS* NKS * 64) void fa_resident_kernel(AttnArgs a, int ntiles_max) {
+template <class TR, int NQS, int L, bool CAUSAL, bool PROBS>
+__global__ __launch_bounds__(NQS * 64) void fa_resident_kernel(AttnArgs a, int ntiles_max) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_dyn[];
-    __shared__ int simd_slots[NQS * NKS];
-    FaResident<TR, NQS, NKS, L, CAUSAL, PROBS>::run(a, lds_dyn, ntiles_max, simd_slots);
+    __shared__ int simd_slots[NQS];
+    FaResident<TR, NQS, L, CAUSAL, PROBS>::run(a, lds_dyn, ntiles_max, simd_slots);
 }
 
 // Dynamic-LDS bytes for a resident launch over all ceil(Sk / 32) key tiles
 // (the last query block of a causal problem sees every key), or 0 when the
 // problem does not fit one workgroup's LDS.
-template <class TR, int NQS, int NKS>
+template <class TR, int NQS>
 inline size_t resident_lds_bytes(const AttnArgs& a) {
-    using R = FaResident<TR, NQS, NKS, 4, false, false>;
+    using R = FaResident<TR, NQS, 4, false, false>;
     const int64_t tiles = ((int64_t)a.Sk + BK - 1) / BK;
-    int64_t body = tiles * R::TILE_ELEMS * (int64_t)sizeof(typename TR::elem);
-    if (body < R::MERGE_BYTES) body = R::MERGE_BYTES;
-    using RP = FaResident<TR, NQS, NKS, 4, false, true>;
+    const int64_t body = tiles * R::TILE_ELEMS * (int64_t)sizeof(typename TR::elem);
+    using RP = FaResident<TR, NQS, 4, false, true>;
     const int64_t bytes = R::HEAD_BYTES + body + (a.probs ? RP::O_TRANS_BYTES : R::O_TRANS_BYTES);
     return (tiles <= 64 && R::HEAD_BYTES + body <= kResidentLdsMax && bytes <= kResidentLdsLimit) ? (size_t)bytes : 0;
 }
 
-template <class TR, int NQS, int NKS, int L, bool CAUSAL, bool PROBS>
+template <class TR, int NQS, int L, bool CAUSAL, bool PROBS>
 hipError_t launch_resident_one(const AttnArgs& args, int ntiles, size_t lds, int64_t grid, hipStream_t stream) {
-    auto kern = fa_resident_kernel<TR, NQS, NKS, L, CAUSAL, PROBS>;
+    auto kern = fa_resident_kernel<TR, NQS, L, CAUSAL, PROBS>;
     // The dynamic-LDS limit is a per-device function attribute: raise it once
     // per device (bit d of attr_set) and instantiation.  Concurrent first calls
     // may both set it, which is harmless.
@@ -478,13 +404,13 @@ hipError_t launch_resident_one(const AttnArgs& args, int ntiles, size_t lds, int
         if (e != hipSuccess) return e;
         attr_set.fetch_or(bit, std::memory_order_release);
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), lds, stream, args, ntiles);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * 64), lds, stream, args, ntiles);
     return hipGetLastError();
 }
 
-template <class TR, int NQS, int NKS, int L>
+template <class TR, int NQS, int L>
 hipError_t launch_resident(const AttnArgs& a, bool causal, hipStream_t stream) {
-    const size_t lds = resident_lds_bytes<TR, NQS, NKS>(a);
+    const size_t lds = resident_lds_bytes<TR, NQS>(a);
     if (lds == 0) return hipErrorInvalidConfiguration;
     const int ntiles = (a.Sk + BK - 1) / BK;
     AttnArgs args = a;
@@ -493,10 +419,10 @@ hipError_t launch_resident(const AttnArgs& a, bool causal, hipStream_t stream) {
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
     const bool probs = a.probs != nullptr;
     if (causal)
-        return probs ? launch_resident_one<TR, NQS, NKS, L, true, true>(args, ntiles, lds, grid, stream)
-                     : launch_resident_one<TR, NQS, NKS, L, true, false>(args, ntiles, lds, grid, stream);
-    return probs ? launch_resident_one<TR, NQS, NKS, L, false, true>(args, ntiles, lds, grid, stream)
-                 : launch_resident_one<TR, NQS, NKS, L, false, false>(args, ntiles, lds, grid, stream);
+        return probs ? launch_resident_one<TR, NQS, L, true, true>(args, ntiles, lds, grid, stream)
+                     : launch_resident_one<TR, NQS, L, true, false>(args, ntiles, lds, grid, stream);
+    return probs ? launch_resident_one<TR, NQS, L, false, true>(args, ntiles, lds, grid, stream)
+                 : launch_resident_one<TR, NQS, L, false, false>(args, ntiles, lds, grid, stream);
 }
 
 }  // namespace fa

@@ -61,11 +61,6 @@ struct Cfg {
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 
-// Whole-row, non-temporal C stores through LDS (see the epilogue).
-#ifndef HIPGPT_GEMM_ROWS_T
-#define HIPGPT_GEMM_ROWS_T 1
-#endif
-
 // KF: K is a multiple of GBK (16-byte path only), so no k-tile runs past K:
 // the k offset of the loads rides in the buffer instruction's scalar offset
 // and the per-element k mask goes away.  With the k loop unrolled by two
@@ -74,12 +69,6 @@ __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f};
 // which matters because fp32 VALU ops take MFMA issue cycles on gfx950.
 // Cache-rotated, us: c1 QKV 32.6 -> 30.6, c1 out 14.9 -> 13.7, c3 QKV
 // 246 -> 232, c3 out 85.2 -> 80.1 (KF alone: c3 QKV 244, c1 level).
-#ifndef HIPGPT_GEMM_KF
-#define HIPGPT_GEMM_KF 1
-#endif
-#ifndef HIPGPT_GEMM_UNROLL2
-#define HIPGPT_GEMM_UNROLL2 1
-#endif
 template <int BM, int BN, int WM, int WN, int GBK, int NACC, bool VEC, bool BF16OUT, bool KF>
 __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(GemmArgs g) {
     using C = Cfg<BM, BN, WM, WN, GBK>;
@@ -228,7 +217,6 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         store(lds);
     }
     __syncthreads();
-#if HIPGPT_GEMM_UNROLL2
     // two k-tiles per iteration, so each stage buffer's address is a constant
     auto step = [&](int kt, auto stage_tag) {
         constexpr int SB = decltype(stage_tag)::value;
@@ -241,20 +229,12 @@ __global__ __launch_bounds__(BM / WM * (BN / WN) * 64) void gemm_bias_kernel(Gem
         step(kt, std::integral_constant<int, 0>{});
         if (kt + 1 < nkt) step(kt + 1, std::integral_constant<int, 1>{});
     }
-#else
-    for (int kt = 0; kt < nkt; ++kt) {
-        if (kt + 1 < nkt) load(kt + 1);
-        compute(lds + (kt & 1) * C::STAGE);
-        if (kt + 1 < nkt) store(lds + ((kt + 1) & 1) * C::STAGE);
-        __syncthreads();
-    }
-#endif
 
     // ---- epilogue, whole-row path: each 32 x 32 block (+ bias) goes through
     // a per-wave scratch in the (now idle) stage buffers and leaves as whole
     // 128-byte row segments, non-temporally, when the block is inside C, fp32,
     // and its 32 columns stay in one segment ----
-    constexpr bool ROWS_T = HIPGPT_GEMM_ROWS_T && VEC && !BF16OUT && C::NW * 32 * 36 <= 2 * C::STAGE;
+    constexpr bool ROWS_T = VEC && !BF16OUT && C::NW * 32 * 36 <= 2 * C::STAGE;
     if constexpr (ROWS_T) {
         float* const X = lds + wave * 32 * 36;
         const int rr = lane >> 3, cc = 4 * (lane & 7);
@@ -358,7 +338,7 @@ hipError_t launch_cfg(const GemmArgs& g, hipStream_t s) {
     if (tiles <= 0 || tiles > 0x7fffffff) return hipErrorInvalidConfiguration;
     constexpr int NT = Cfg<BM, BN, WM, WN, GBK>::NT;
     const dim3 grid((unsigned)tiles), block(NT);
-    const bool kf = HIPGPT_GEMM_KF && VEC && g.K % GBK == 0;
+    const bool kf = VEC && g.K % GBK == 0;
     if (g.out_bf16) {
         if (kf)
             hipLaunchKernelGGL((gemm_bias_kernel<BM, BN, WM, WN, GBK, NACC, VEC, true, VEC>), grid, block, 0, s, g);

@@ -38,16 +38,8 @@
 namespace hipgpt {
 
 // Weighted-sum output stores: whole 128-byte row segments per half-wave,
-// written non-temporally with HIPGPT_HELPERS_NT (a8: 21.6 -> 20.1 us).
-#ifndef HIPGPT_HELPERS_NT
-#define HIPGPT_HELPERS_NT 1
-#endif
-__device__ __forceinline__ void nt_store(float* p, float v) {
-    if (HIPGPT_HELPERS_NT)
-        __builtin_nontemporal_store(v, p);
-    else
-        *p = v;
-}
+// written non-temporally (a8: 21.6 -> 20.1 us against plain stores).
+__device__ __forceinline__ void nt_store(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
 namespace {
 
@@ -241,14 +233,11 @@ struct WsumTile {
     }
 };
 
-// P of the weighted sum through a per-wave LDS transpose, whole 128-byte rows
-// per load (1), or straight in the MFMA operand layout, 32 bytes of each of
-// 32 rows per load (0).  a8, cache-rotated: 20.1 -> 19.6 us (mean of four).
-// Deeper P prefetch (3 or 4 tiles in flight instead of 2) measured slower
-// either way, and so did requesting V of the next tile before P.
-#ifndef HIPGPT_WSUM_TRANS
-#define HIPGPT_WSUM_TRANS 1
-#endif
+// P of the weighted sum goes through a per-wave LDS transpose, whole 128-byte
+// rows per load, instead of straight in the MFMA operand layout (32 bytes of
+// each of 32 rows per load): a8, cache-rotated, 20.1 -> 19.6 us (mean of
+// four).  Deeper P prefetch (3 or 4 tiles in flight instead of 2) measured
+// slower either way, and so did requesting V of the next tile before P.
 
 // Workgroup (sequence b, query group qg); wave w owns query tile qg*4 + w
 // over all keys; V tiles staged through LDS (double-buffered, one barrier per
@@ -258,7 +247,6 @@ __global__ __launch_bounds__(256) void wsum_tiles_kernel(const float* __restrict
                                                          float* __restrict__ O, int S, int n_qg) {
     constexpr int NB = DP / 32;
     constexpr int NL = DP / 32;  // float4 per thread per staged V tile
-    using T [[maybe_unused]] = WsumTile<DP>;
     __shared__ float vs[2][32 * DP];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 31, hf = lane >> 5;
@@ -266,8 +254,6 @@ __global__ __launch_bounds__(256) void wsum_tiles_kernel(const float* __restrict
     const int qg = lid % n_qg, b = lid / n_qg;
     const int q0 = (qg * 4 + wave) * 32;
     const int nt = (S + 31) / 32;
-    const bool qok = q0 + c < S;
-    [[maybe_unused]] const float* prow = P + ((int64_t)b * S + (qok ? q0 + c : 0)) * S + hf * 16;
     const float* Vb = V + (int64_t)b * S * DP;
 
     floatx4 vr[NL];
@@ -293,7 +279,6 @@ __global__ __launch_bounds__(256) void wsum_tiles_kernel(const float* __restrict
     for (int db = 0; db < NB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-#if HIPGPT_WSUM_TRANS
     // P through a per-wave LDS transpose: each load instruction reads 8 whole
     // 128-byte rows of the tile (lane: row rr + 8i, keys cc .. cc+3), and the
     // MFMA operands (lane: query c, keys 16hf .. 16hf+15) are read back from
@@ -318,36 +303,19 @@ __global__ __launch_bounds__(256) void wsum_tiles_kernel(const float* __restrict
         for (int g = 0; g < 4; ++g) op[g] = *reinterpret_cast<const floatx4*>(X + c * 36 + 16 * hf + 4 * g);
         asm volatile("" ::: "memory");  // the next tile's writes come after these reads
     };
-#endif
     floatx4 pa[4], pb[4];  // P of tiles kt and kt + 1
-#if HIPGPT_WSUM_TRANS
     load_tile(pa, 0);
     if (1 < nt) load_tile(pb, 1);
-#else
-    T::load_p(pa, prow, qok, 0, hf, S);
-    if (1 < nt) T::load_p(pb, prow, qok, 1, hf, S);
-#endif
     load_v(0);
     store_v(0);
     __syncthreads();
     for (int kt = 0; kt < nt; ++kt) {
         const int buf = kt & 1;
         floatx4 cur[4];
-#if HIPGPT_WSUM_TRANS
         operands(pa, cur);
-#else
-#pragma unroll
-        for (int g = 0; g < 4; ++g) cur[g] = pa[g];
-#endif
 #pragma unroll
         for (int g = 0; g < 4; ++g) pa[g] = pb[g];
-        if (kt + 2 < nt) {
-#if HIPGPT_WSUM_TRANS
-            load_tile(pb, kt + 2);
-#else
-            T::load_p(pb, prow, qok, kt + 2, hf, S);
-#endif
-        }
+        if (kt + 2 < nt) load_tile(pb, kt + 2);
         if (kt + 1 < nt) load_v(kt + 1);
         const float* vp = &vs[buf][(hf * 16) * DP + c];
 #pragma unroll

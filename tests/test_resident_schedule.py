@@ -9,15 +9,15 @@ it would hang (the wait would run out and the wave compute on an unpublished
 tile).  This test restates each wave's sequence of counter bumps, waits and
 barriers and runs them under an event scheduler (always one runnable wave,
 fixed or randomised choice).  It checks, for every shape the resident kernel
-serves (S <= 256 at 32-row tiles, causal or not, probs or not, NKS = 1 or 2,
-ring depth L = 2 or 4, every launch rank): every wave finishes, and every
-tile is published exactly NW times.
+serves (S <= 256 at 32-row tiles, causal or not, probs or not, ring depth
+L = 2 or 4, every launch rank): every wave finishes, and every tile is
+published exactly NW times.
 
 Restated from FaResident::run: tiles T = ceil(min(q0 + 256, Sq) + off) / 32)
 (causal) or ceil(Sk / 32); wave tiles wtiles from tile_range; issue(0..L-1),
 ahead(t < L) = publish t; step(t): publish t + L if t + L < T, then, when
-t < wtiles and t % NKS == ks, wait cnt[t] >= NW; after the loop the probs
-(NKS > 1) and split merges are workgroup barriers.
+t < wtiles, wait cnt[t] >= NW.  Waves 2j and 2j+1 of the SIMD ranking take
+sub-blocks j and 7-j.
 """
 import random
 
@@ -37,16 +37,15 @@ def wtiles_of(q0, qw0, Sq, Sk, off, causal):
     return ntiles, wt
 
 
-def wave_programs(Sq, Sk, causal, probs, nks, L, rank, n_qblk):
-    nw = NQS * nks
+def wave_programs(Sq, Sk, causal, probs, L, rank, n_qblk):
+    nw = NQS
     off = Sk - Sq if causal else 0
     qb = n_qblk - 1 - rank if causal else rank
     q0 = qb * NQS * QW
     waves = []
     for rk in range(nw):
-        simd, grp = rk // (nw // 4), rk % (nw // 4)
-        sub = NQS - 1 - simd if grp & 1 else simd
-        ks = grp >> 1
+        simd = rk // 2
+        sub = NQS - 1 - simd if rk & 1 else simd
         qw0 = q0 + sub * QW
         T, wt = wtiles_of(q0, qw0, Sq, Sk, off, causal)
         ops = [("barrier", 0)]  # the counters' clear is published by a barrier
@@ -55,12 +54,8 @@ def wave_programs(Sq, Sk, causal, probs, nks, L, rank, n_qblk):
         for t in range(T):
             if t + L < T:
                 ops.append(("pub", t + L))
-            if t < wt and t % nks == ks:
+            if t < wt:
                 ops.append(("wait", t))
-        if probs and nks > 1:
-            ops.append(("barrier", 1))
-        if nks > 1:
-            ops += [("barrier", 2), ("barrier", 3)]
         waves.append(ops)
     return waves, nw
 
@@ -103,14 +98,13 @@ def run(waves, nw, rng=None):
 
 
 @pytest.mark.parametrize("L", [2, 4])
-@pytest.mark.parametrize("nks", [1, 2])
 @pytest.mark.parametrize("probs", [False, True])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("S", [1, 31, 32, 33, 64, 100, 200, 255, 256])
-def test_every_tile_wait_ends(S, causal, probs, nks, L):
+def test_every_tile_wait_ends(S, causal, probs, L):
     n_qblk = (S + NQS * QW - 1) // (NQS * QW)
     for rank in range(n_qblk):
-        waves, nw = wave_programs(S, S, causal, probs, nks, L, rank, n_qblk)
+        waves, nw = wave_programs(S, S, causal, probs, L, rank, n_qblk)
         T = max(sum(1 for k, _ in ops if k == "pub") for ops in waves)
         for rng in [None] + [random.Random(seed) for seed in range(10)]:
             blocked, cnt = run(waves, nw, rng)
@@ -121,7 +115,7 @@ def test_every_tile_wait_ends(S, causal, probs, nks, L):
 def test_a_missing_publication_is_caught():
     """The checker itself: drop one wave's publication of tile 1 and the
     schedule must block (a wave waits on tile 1 forever)."""
-    waves, nw = wave_programs(256, 256, True, False, 1, 4, 0, 1)
+    waves, nw = wave_programs(256, 256, True, False, 4, 0, 1)
     victim = waves[3]
     waves[3] = [op for op in victim if op != ("pub", 1)]
     blocked, _ = run(waves, nw)
