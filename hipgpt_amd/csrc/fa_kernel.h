@@ -405,19 +405,38 @@ struct FaKernel {
         // computed, then written to the other LDS buffer.  (Two stages of
         // register prefetch measured no faster at any head dim and cost an
         // occupancy step at D = 32.)
+        // With probs, the max/sum sweep (MODE 1) requests the probs sweep's first stage during its last one, so
+        // the probs sweep (MODE 2) starts from registers instead of a memory round trip.
+        constexpr bool WV2 = true, WK2 = !SPILL;  // what the probs sweep stages
         auto sweep = [&](auto mode_tag, float mlog, float* prow, bool pvec) {
-            constexpr bool WV = decltype(mode_tag)::value != 1;  // the max/sum sweep stages no V
-            constexpr bool WK = !(SPILL && decltype(mode_tag)::value == 2);  // nor the spilled probs sweep K
+            constexpr int MODE = decltype(mode_tag)::value;
+            constexpr bool WV = MODE != 1;              // the max/sum sweep stages no V
+            constexpr bool WK = !(SPILL && MODE == 2);  // nor the spilled probs sweep K
             if (nstages > 0) {
-                st.template load<WV, WK>(0, tid);
+                if (MODE != 2) st.template load<WV, WK>(0, tid);
                 st.template store<WV, WK>(lds, tid);
             }
             __syncthreads();
-            for (int i = 0; i < nstages; ++i) {
-                if (i + 1 < nstages) st.template load<WV, WK>(i + 1, tid);
-                compute(mode_tag, i, mlog, prow, pvec);
-                if (i + 1 < nstages) st.template store<WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
-                __syncthreads();
+            if constexpr (MODE == 1) {
+                // the last stage peeled: it requests the probs sweep's first stage
+                for (int i = 0; i + 1 < nstages; ++i) {
+                    st.template load<WV, WK>(i + 1, tid);
+                    compute(mode_tag, i, mlog, prow, pvec);
+                    st.template store<WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                    __syncthreads();
+                }
+                if (nstages > 0) {
+                    st.template load<WV2, WK2>(0, tid);
+                    compute(mode_tag, nstages - 1, mlog, prow, pvec);
+                    __syncthreads();
+                }
+            } else {
+                for (int i = 0; i < nstages; ++i) {
+                    if (i + 1 < nstages) st.template load<WV, WK>(i + 1, tid);
+                    compute(mode_tag, i, mlog, prow, pvec);
+                    if (i + 1 < nstages) st.template store<WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                    __syncthreads();
+                }
             }
         };
 
@@ -427,7 +446,8 @@ struct FaKernel {
         auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
             if (nstages > 0) {
-                st.template load<SECOND, !SECOND>(0, tid);
+                // the probs sweep's first V stage was requested in the max/sum sweep's first stage
+                if (!SECOND) st.template load<false, true>(0, tid);
                 st.template store<SECOND, !SECOND>(lds, tid);
             }
             __syncthreads();
@@ -436,6 +456,7 @@ struct FaKernel {
                     constexpr int I = decltype(ic)::value;
                     if (I < nstages) {
                         if (I + 1 < nstages) st.template load<SECOND, !SECOND>(I + 1, tid);
+                        if (!SECOND && I == 0) st.template load<true, false>(0, tid);  // V of the probs sweep's first stage
                         const E* cur = lds + (I & 1) * STAGE_ELEMS;
                         const int t = I * NKS + ks;
                         if (t < wtiles) {
