@@ -95,6 +95,7 @@ CONFIGS = {
     "d256": (4, 8, 1024, 1024, 256, True, "f32", False, "fwd"),
     "d256_legacy": (4, 8, 1024, 1024, 256, False, "f32", True, "fwd"),
     "d256_bwd_legacy": (4, 8, 1024, 1024, 256, False, "f32", True, "bwd"),
+    "d512": (2, 4, 1024, 1024, 512, True, "f32", False, "fwd"),
     # The probs-free training pair at the same shapes: forward writing O and the
     # row log-sum-exp, and the backward that recomputes P from it.
     "c1_fwd_lse": (32, 8, 256, 256, 32, True, "f32", False, "fwd_lse"),

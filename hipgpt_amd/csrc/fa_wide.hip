@@ -1,26 +1,29 @@
 // fa_wide.hip -- fp32 attention forward on gfx950 MFMA for head dims above
-// 128 (128 < D <= 256, D % 4 == 0, 16-byte aligned rows; padded to 256).
+// 128 (128 < D <= 512, D % 4 == 0, 16-byte aligned rows; padded to 256 or 512).
 //
 // Replaces, for those head dims, multihead_attention_kernel_fallback (HipGPT
 // src/hip_kernels.cpp:329-402), the reference's path for any head dim other
 // than 32 and 64.  The per-wave kernel of fa_kernel.h holds a wave's 32 query
 // rows of Q and of the O accumulator in registers, D/2 + D/2 values per lane,
 // which stops fitting above D = 128.  Here the head dim is split instead:
-//   * the DH = 4 waves of a query sub-block share its 32 queries and each
-//     holds 64 of the 256 head dims of Q (pre-scaled by scale*log2 e) and of
-//     the O accumulator;
+//   * the DH waves of a query sub-block (4 at padded D = 256, 8 at 512) share
+//     its 32 queries and each holds 64 of the head dims of Q (pre-scaled by
+//     scale*log2 e) and of the O accumulator;
 //   * per key tile, each wave forms its partial S^T = K Q^T over its dims,
-//     the four partials go through LDS and every wave adds them in the same
-//     order, so the four hold the same scores bit for bit and run the same
+//     the DH partials go through LDS and every wave adds them in the same
+//     order, so all of them hold the same scores bit for bit and run the same
 //     online softmax (lazy rescale, as fa_kernel.h); then each wave
 //     accumulates O^T += V^T P^T for its own dims.
 // K and V tiles are row-major in LDS (rowtiles.h) in one stage buffer: the
 // next stage waits in registers during the MFMAs and is stored after a
-// barrier (two buffers would not fit next to the partial-score exchange).
+// barrier (two buffers would not fit next to the partial-score exchange).  At
+// padded D = 512 one K and one V tile do not fit together either: the V tile
+// of key tile t is requested during its scores and stored over the K tile
+// once every wave has read it, and K of tile t+1 is requested during P V.
 // With probs (the drop-in contract): sweep 1 forms each row's max and sum
 // (K tiles only); sweep 2 recomputes the scores, stores P = exp2(s' - m -
-// log2 l) -- wave dh storing register group dh, one store per element -- and
-// accumulates P V.  Causal: key tiles past a sub-block's diagonal are skipped,
+// log2 l) -- every element by exactly one of the DH waves -- and accumulates
+// P V.  Causal: key tiles past a sub-block's diagonal are skipped,
 // the diagonal tiles masked, and the probs above the diagonal stored as 0.
 #include "common.h"
 #include "fa_common.h"
@@ -35,23 +38,22 @@ using fa::acc_key;
 using fa::kLazyMax;
 using fa::QW;
 
-constexpr int kWideDP = 256;
-constexpr int kWideDH = 4;
-
-template <int NQB, bool CAUSAL, bool PROBS>
+template <int DP, int DH, int NQB, bool CAUSAL, bool PROBS>
 struct WideFwd {
-    using T = RowTiles<kWideDP, kWideDH>;
-    static constexpr int NW = NQB * kWideDH;
+    using T = RowTiles<DP, DH>;
+    static_assert(DH == 4 || DH == 8, "probs stores split over 4 or 8 waves");
+    static constexpr bool SPLIT = DP > 256;  // K and V tiles take turns in the stage buffer
+    static constexpr int NW = NQB * DH;
     static constexpr int NT = NW * 64;
-    static constexpr int STAGE = 2 * T::ROW;  // K, V (row-major)
-    static constexpr int XCH = NW * 16 * 64;   // partial score tiles
+    static constexpr int STAGE = (SPLIT ? 1 : 2) * T::ROW;  // K (, V) row-major
+    static constexpr int XCH = NW * 16 * 64;                 // partial score tiles
     static constexpr int LDS_FLOATS = STAGE + XCH;
 
     __device__ __forceinline__ static void run(const AttnArgs& a, float* lds) {
         const int tid = threadIdx.x, lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31, hf = lane >> 5;
-        const int sb = wave / kWideDH, dh = wave % kWideDH;
+        const int sb = wave / DH, dh = wave % DH;
         const int BH = a.B * a.H;
         const int bh = blockIdx.x % BH;
         const int rank = blockIdx.x / BH;
@@ -112,16 +114,26 @@ struct WideFwd {
         // alone).  2: probs stored with the final (m, l) + P V.
         auto sweep = [&](auto mode_tag, float mlog, float* prow, bool pvec) {
             constexpr int MODE = decltype(mode_tag)::value;
-            RowStage<kWideDP, NT, MODE == 1 ? 1 : 2> stg;
+            constexpr bool TURNS = SPLIT && MODE != 1;  // V takes K's place after the scores
+            RowStage<DP, NT, (SPLIT || MODE == 1) ? 1 : 2> stg;
+            const float* const vt = lds + (SPLIT ? 0 : T::ROW);
             if (nstages > 0) {
                 stg.load(kl, vl, 0, D, tid);
                 stg.store(lds, T::ROW, tid);
             }
             __syncthreads();
             for (int t = 0; t < nstages; ++t) {
-                if (t + 1 < nstages) stg.load(kl, vl, (t + 1) * BK, D, tid);
+                if constexpr (TURNS)
+                    stg.load(vl, vl, t * BK, D, tid);  // V of this tile, in flight during its scores
+                else if (t + 1 < nstages)
+                    stg.load(kl, vl, (t + 1) * BK, D, tid);
                 const bool act = t < wtiles;  // wave-uniform
-                floatx16 s = scores(act, t);
+                floatx16 s = scores(act, t);   // past its barrier no wave reads this K tile again
+                if constexpr (TURNS) {
+                    stg.store(lds, T::ROW, tid);
+                    __syncthreads();
+                    if (t + 1 < nstages) stg.load(kl, vl, (t + 1) * BK, D, tid);  // next K, during P V
+                }
                 if (act) {
                     if constexpr (MODE == 0) {
                         const float tmax = fa::tile_max(s);
@@ -142,7 +154,7 @@ struct WideFwd {
                             ls += s[r];
                         }
                         l_run += ls;  // this lane half's partial; the halves are summed after the sweep
-                        T::template rchain<1>(o, lds + T::ROW, &s, c, hf, dh);
+                        T::template rchain<1>(o, vt, &s, c, hf, dh);
                     } else if constexpr (MODE == 1) {
                         const float m_new = fa::vmax(m_run, fa::tile_max(s));
                         float ls = 0.f;
@@ -153,13 +165,15 @@ struct WideFwd {
                     } else {
 #pragma unroll
                         for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r] - mlog);
-                        if (qi < Sq) {
-                            // wave dh stores register group dh (keys 8*dh + 4h .. +3)
-                            const int k0 = t * BK + 8 * dh + 4 * hf;
+                        // wave dh stores register group gs (keys 8*gs + 4h .. +3): DH = 4,
+                        // gs = dh; DH = 8, gs = dh / 2 on the lane half h = dh % 2
+                        const int gs = DH == 4 ? dh : dh >> 1;
+                        if (qi < Sq && (DH == 4 || hf == (dh & 1))) {
+                            const int k0 = t * BK + 8 * gs + 4 * hf;
                             floatx4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                             for (int g = 0; g < 4; ++g)
-                                if (g == dh) v = floatx4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
+                                if (g == gs) v = floatx4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]};
                             if (pvec && k0 + 3 < Sk) {
                                 *reinterpret_cast<floatx4*>(prow + k0) = v;
                             } else {
@@ -168,7 +182,7 @@ struct WideFwd {
                                     if (k0 + j < Sk) prow[k0 + j] = v[j];
                             }
                         }
-                        T::template rchain<1>(o, lds + T::ROW, &s, c, hf, dh);
+                        T::template rchain<1>(o, vt, &s, c, hf, dh);
                     }
                 }
                 __syncthreads();  // every wave is done with the stage and the exchange
@@ -213,30 +227,34 @@ struct WideFwd {
     }
 };
 
-template <int NQB, bool CAUSAL, bool PROBS>
-__global__ __launch_bounds__(NQB* kWideDH * 64) void fa_wide_kernel(AttnArgs a) {
-    using K = WideFwd<NQB, CAUSAL, PROBS>;
+template <int DP, int DH, int NQB, bool CAUSAL, bool PROBS>
+__global__ __launch_bounds__(NQB* DH * 64) void fa_wide_kernel(AttnArgs a) {
+    using K = WideFwd<DP, DH, NQB, CAUSAL, PROBS>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     K::run(a, lds);
 }
 
-// Query sub-blocks per workgroup (4 waves each).
-constexpr int kWideNQB = 2;
+// Eight waves per workgroup: padded D = 256 two query sub-blocks of four
+// waves, D = 512 one of eight.
+template <int DP, int DH, int NQB, bool CAUSAL, bool PROBS>
+hipError_t launch_wide_one(const AttnArgs& a, hipStream_t s) {
+    AttnArgs args = a;
+    args.n_qblk = (a.Sq + NQB * QW - 1) / (NQB * QW);
+    const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
+    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((fa_wide_kernel<DP, DH, NQB, CAUSAL, PROBS>), dim3((unsigned)grid), dim3(NQB * DH * 64), 0, s,
+                       args);
+    return hipGetLastError();
+}
 
 template <bool CAUSAL, bool PROBS>
 hipError_t launch_wide(const AttnArgs& a, hipStream_t s) {
-    AttnArgs args = a;
-    args.n_qblk = (a.Sq + kWideNQB * QW - 1) / (kWideNQB * QW);
-    const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
-    if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((fa_wide_kernel<kWideNQB, CAUSAL, PROBS>), dim3((unsigned)grid), dim3(kWideNQB * kWideDH * 64),
-                       0, s, args);
-    return hipGetLastError();
+    return a.D <= 256 ? launch_wide_one<256, 4, 2, CAUSAL, PROBS>(a, s) : launch_wide_one<512, 8, 1, CAUSAL, PROBS>(a, s);
 }
 
 }  // namespace
 
-bool fa_wide_supported(int D) { return D > 128 && D <= kWideDP && D % 4 == 0; }
+bool fa_wide_supported(int D) { return D > 128 && D <= 512 && D % 4 == 0; }
 
 hipError_t launch_fa_wide(const AttnArgs& a, bool causal, hipStream_t stream) {
     if (!fa_wide_supported(a.D)) return hipErrorInvalidValue;

@@ -318,13 +318,15 @@ def test_unfused_helpers_unaligned_views(dev):
     assert np.abs(host(out).reshape(B * S, D) - wo).max() <= TOL_O
 
 
-# Head dims above 128 with D % 4 == 0 run the head-dim-split MFMA kernel
-# (fa_wide.hip; four waves per 32 queries, 64 dims each, padded to 256); other
-# D above 128 the one-wave-per-row kernel (generic.hip).  S below, across and
+# Head dims above 128 with D % 4 == 0 up to 512 run the head-dim-split MFMA
+# kernel (fa_wide.hip; 64 dims per wave, four waves per 32 queries padded to
+# 256, eight padded to 512); other D above 128 the one-wave-per-row kernel
+# (generic.hip).  S below, across and
 # off the 32-row tile, several query blocks per (b, h), Sq < Sk.
 WIDE_FWD = [
     (2, 33, 33, 2, 132), (1, 1, 1, 2, 256), (1, 70, 70, 3, 160), (2, 130, 130, 2, 192), (1, 257, 257, 1, 256),
     (1, 100, 100, 2, 200), (2, 40, 90, 2, 256), (1, 300, 300, 1, 228), (1, 64, 64, 2, 150), (1, 9, 40, 2, 260),
+    (1, 70, 70, 2, 512), (2, 33, 100, 1, 384), (1, 130, 130, 1, 300), (1, 1, 1, 1, 512), (1, 40, 40, 1, 520),
 ]
 
 
@@ -350,9 +352,9 @@ def test_wide_head_dim_forward_matches_oracle(dev, B, Sq, Sk, H, D, causal):
     assert np.abs(host(out2) - want_o).max() <= TOL_O
 
 
-@pytest.mark.parametrize("B,S,E,H", [(2, 130, 512, 2), (1, 300, 640, 4), (1, 77, 1024, 4)])
+@pytest.mark.parametrize("B,S,E,H", [(2, 130, 512, 2), (1, 300, 640, 4), (1, 77, 1024, 4), (1, 100, 1024, 2)])
 def test_wide_head_dim_dropin_matches_reference_launcher(dev, B, S, E, H):
-    """HipGPT's call at D = 256, 160, 256: against the reference's launcher
+    """HipGPT's call at D = 256, 160, 256, 512: against the reference's launcher
     (its fallback kernel) on the same device buffers, with and without probs."""
     ref = _ref_or_skip()
     qkv = O.seeded_planar(171 + S + E, B, S, E)
