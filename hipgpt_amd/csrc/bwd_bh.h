@@ -578,6 +578,7 @@ __device__ __forceinline__ int opaque(int v) {
     return v;
 }
 
+template <bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -622,18 +623,28 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     RowLoader kl, vl;
     kl.init(a.k + base, a.ts, S, D);
     vl.init(a.v + base, a.ts, S, D);
+    // Causal probs: query tiles before the wave's key tile (t < wave) hold
+    // P = 0, so their tiles are neither read nor computed with; the wave's P
+    // pipeline holds zeros there.
+    const bool p0 = !CAUSAL || wave == 0, p1 = !CAUSAL || wave <= 1;
     if (active) {
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) vv[s] = vl.load(kj, hf * (D / 8) + s);
-        load_p_tile(p, pr, 0, kj, kval, hf, S);
+        if (p0) {
+            load_p_tile(p, pr, 0, kj, kval, hf, S);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = 0.f;
+        }
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) kv[s] = kl.load(kj, hf * (D / 8) + s);
     }
     ring_store(0, r0);
     ring_store(1, r1);
-    if (!active) {
-        // a wave past the last key tile zeroes its partial-sum and dQ-term
-        // slots once, so the sums over all NW waves need no selects
+    if (!active || CAUSAL) {
+        // a wave past the last key tile (causal: every wave, whose first
+        // steps contribute nothing) zeroes its partial-sum and dQ-term slots
+        // once, so the sums over all NW waves need no selects
         lds[nc::PD + (hf * NW + wave) * BK + c] = 0.f;
 #pragma unroll
         for (int k = 0; k < 2 * BK * (BK / 4) / 64; ++k) {
@@ -693,8 +704,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
         for (int s = 0; s < D / 8; ++s)
 #pragma unroll
             for (int j = 0; j < 4; ++j) vr[4 * s + j] = vv[s][j];
-        dp = dp_tile(slot(0) + nc::TILE);
-        partial(std::integral_constant<int, 0>{}, p, dp);
+        if (p0) {
+            dp = dp_tile(slot(0) + nc::TILE);
+            partial(std::integral_constant<int, 0>{}, p, dp);
+        }
     }
 
     // dQ rows of query tile i (parity PAR): wave w adds rows 4w .. 4w+3 of the
@@ -724,7 +737,14 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     lds_barrier();  // step 0's partial row sums
     floatx4 rn = ring_load(2);
     if (active) {
-        if (nt > 1) load_p_tile(pn, pr, 1, kj, kval, hf, S);
+        if (nt > 1) {
+            if (p1) {
+                load_p_tile(pn, pr, 1, kj, kval, hf, S);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) pn[r] = 0.f;
+            }
+        }
         // K through the scratch (the partial sums' reads of it are done)
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) *reinterpret_cast<floatx4*>(X + c * XP + hf * (D / 2) + 4 * s) = kv[s];
@@ -783,6 +803,30 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) dqw[PAR * NW * BK * PP + (8 * (r >> 2) + (r & 3)) * PP] = aq[r];
     };
+    // Causal: the step of a wave whose keys all follow query tile t.  Its
+    // terms are zero (the slots hold zeros); it keeps the P pipeline (P of
+    // tile t+2, zero while that tile is still before the wave's keys) and, one
+    // step before its first tile, forms that tile's dP and partial row sums.
+    auto idle_step = [&](auto par_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dnx) {
+        constexpr int PAR = decltype(par_tag)::value;
+        if (t + 1 == wave) {
+            dnx = dp_tile(slot(t + 1) + nc::TILE);
+            partial(std::integral_constant<int, 1 - PAR>{}, pnx, dnx);
+        }
+        if (t + 2 >= wave) {
+            load_p_tile(pc, pr, t + 2 < nt ? t + 2 : nt - 1, kj, kval, hf, S);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pc[r] = 0.f;
+        }
+    };
+    auto run_step = [&](auto last_tag, auto par_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dc, floatx16& dnx) {
+        if (!active) return;
+        if (!CAUSAL || t >= wave)
+            step(last_tag, par_tag, t, pc, pnx, dc, dnx);
+        else
+            idle_step(par_tag, t, pc, pnx, dnx);  // t < wave <= nt - 1: never the last step
+    };
     // Every wave after its step on tile t: the dQ rows of tile t-1, the ring,
     // the barrier.
     auto finish = [&](auto par_tag, int t) {
@@ -796,19 +840,19 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     using Odd = std::integral_constant<int, 1>;
     int t = 0;
     for (; t + 2 < nt; t += 2) {
-        if (active) step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
+        run_step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
         finish(Even{}, t);
-        if (active) step(std::false_type{}, Odd{}, t + 1, pn, p, dpn, dp);
+        run_step(std::false_type{}, Odd{}, t + 1, pn, p, dpn, dp);
         finish(Odd{}, t + 1);
     }
     if (t + 1 < nt) {
-        if (active) step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
+        run_step(std::false_type{}, Even{}, t, p, pn, dp, dpn);
         finish(Even{}, t);
-        if (active) step(std::true_type{}, Odd{}, t + 1, pn, p, dpn, dp);
+        run_step(std::true_type{}, Odd{}, t + 1, pn, p, dpn, dp);
         finish(Odd{}, t + 1);
         reduce_dq(Odd{}, t + 1);
     } else {
-        if (active) step(std::true_type{}, Even{}, t, p, pn, dp, dpn);
+        run_step(std::true_type{}, Even{}, t, p, pn, dp, dpn);
         finish(Even{}, t);
         reduce_dq(Even{}, t);
     }
@@ -861,20 +905,25 @@ hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
+template <bool CAUSAL>
+hipError_t launch_bh_probs_mode(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
     static std::atomic<unsigned long long> attr_set{0};
-    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(bh::bwd_bh_probs_kernel), bh::nc::kLdsBytes, attr_set);
+    auto kern = bh::bwd_bh_probs_kernel<CAUSAL>;
+    hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(kern), bh::nc::kLdsBytes, attr_set);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(bh::bwd_bh_probs_kernel, dim3((unsigned)grid), dim3(bh::NW * 64), bh::nc::kLdsBytes, s, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(bh::NW * 64), bh::nc::kLdsBytes, s, a);
     return hipGetLastError();
 }
 
+inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
+    return a.causal ? launch_bh_probs_mode<true>(a, s) : launch_bh_probs_mode<false>(a, s);
+}
+
 inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
-    // stored probs without a causal mask: the single-read kernel
-    if (a.probs && !a.causal) return launch_bh_probs(a, s);
-    if (a.probs) return a.causal ? launch_bh_mode<true, true>(a, s) : launch_bh_mode<false, true>(a, s);
+    // stored probs: the single-read kernel
+    if (a.probs) return launch_bh_probs(a, s);
     return a.causal ? launch_bh_mode<true, false>(a, s) : launch_bh_mode<false, false>(a, s);
 }
 
