@@ -124,8 +124,9 @@ void launch_attention_weighted_sum(const float* softmax, const float* V, float* 
 // Attention backward (src/hip_kernels.cpp:1245-1272).  The planar buffers of
 // the forward; the B*H*S row-dot workspace comes from the caller or, for the
 // drop-in symbol (whose signature has no workspace), from a buffer cached per
-// device and grown on demand -- only for shapes whose kernels use it (not
-// D = 32 with S <= 256, S % 4 == 0, which forms the row dots in LDS).
+// device and grown on demand -- only for shapes whose kernels use it (not,
+// e.g., D = 32 with S <= 256, whose per-(b, h) kernel forms the row dots in
+// LDS).
 namespace {
 
 hipgpt::BwdArgs planar_bwd_args(const float* go, const float* qkv, const float* probs, float* gqkv, int B, int S,

@@ -1,8 +1,9 @@
 // bwd_bh.h -- attention backward with one workgroup per (b, h), for head
 // dim 32 and S <= 256: the shape of HipGPT's default model
 // (src/train_gpt.cpp:175-180), whose backward is src/hip_kernels.cpp:1159-1272.
-// Two modes: probs-free (P rebuilt from the forward's O and row lse) and the
-// reference's contract (P read from the stored probs; see PROBS below).
+// Two kernels: bwd_bh_kernel rebuilds P from the forward's O and row lse;
+// bwd_bh_probs_kernel (below) reads the stored probs, the reference's
+// contract.
 //
 // One (b, h) problem fits one CU: Q and dO rows, the row log-sum-exp and
 // Dq = dO . O stay in LDS for the whole launch, and each of the 8 waves keeps
@@ -28,17 +29,6 @@
 // bounded besides.  Each wave stages its own diagonal query tile (Q, dO
 // rows, lse', Dq = dO . O) and flags it, so no workgroup-wide barrier follows
 // the start.  The summation order is fixed: results are deterministic.
-//
-// PROBS (the stored [S][S] probs instead of O and lse): P is read from
-// memory instead of rebuilt, and Dq = sum_j P_ij dP_ij = dO_i . (P V)_i needs
-// O = P V first.  Phase 1 gives each query tile's O to one wave, which sums
-// the key tiles' P V terms in registers (16 MFMAs per key tile, V rows read
-// as it goes), forms the tile's Dq and flags it; phase 2 (the jobs above,
-// with the loaded P) waits per tile for that flag.  Causally the light wave
-// of each SIMD pair owns both of the pair's query tiles, the heavy partner's
-// first, so the wave with the most phase-2 jobs starts them at once.  P is
-// read twice (once per phase).  Without the causal mask (the reference's
-// drop-in call) bwd_bh_probs_kernel below runs instead and reads P once.
 //
 // One launch, no atomics, no workspace; the LDS footprint (154 KB at
 // S = 256) allows one workgroup per CU, two waves per SIMD, and the causal
@@ -155,14 +145,13 @@ __device__ __forceinline__ void load_p_tile(floatx16& pv, __amdgpu_buffer_rsrc_t
     }
 }
 
-template <bool CAUSAL, bool PROBS>
+template <bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     const unsigned long long t_start = __builtin_amdgcn_s_memrealtime();
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ int simd_slots[NW];
     __shared__ int staged[NW];  // query tile t's rows are in LDS
     __shared__ int chain[NW];   // contributions summed into query tile t's dQ partial
-    __shared__ int dqready[NW]; // stored probs: Dq of query tile t is in LDS
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, hf = lane >> 5;
@@ -178,7 +167,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     float* const X = lds + L.x + wave * BK * XP;
     const int64_t base = (int64_t)b * a.bs + (int64_t)h * a.hs;
 
-    if (tid < NW) staged[tid] = chain[tid] = dqready[tid] = 0;
+    if (tid < NW) staged[tid] = chain[tid] = 0;
     // Key tile of this wave: SIMD s (ranks 2s, 2s+1) takes tiles s and
     // nt-1-s, so causal work pairs up to nt + 1 tiles per SIMD.  The rank's
     // barrier also publishes the cleared flags.
@@ -187,12 +176,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     int kt = -1;
     if (s2 < (nt + 1) / 2) kt = (sr & 1) ? (nt - 1 - s2 > s2 ? nt - 1 - s2 : -1) : s2;
     if (kt < 0) return;
-    // Stored probs, causal: the SIMD's light wave (key tile nt-1-s2, s2 + 1
-    // jobs) runs the phase-1 work of both tiles; the heavy one (key tile s2)
-    // goes straight to phase 2.
-    const bool light = PROBS && CAUSAL && (sr & 1);
-    const bool p1_off = PROBS && CAUSAL && !(sr & 1) && nt - 1 - s2 > s2;
-    const int kp = s2;  // a light wave's partner
 
     // Causal: key tile kt first needs query tile kt + t at its step t, and the
     // wave of key tile 0 has the most steps.  Starting wave kt's loads kt
@@ -202,7 +185,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
     // of them.  s_memrealtime counts 10 ns; the wait is at most 7 slots.
     // Only the first set of workgroups, which the device starts together,
     // loads in a burst; later ones start as slots free up and are not delayed.
-    if (!PROBS && CAUSAL && kt > 0 && bhi < a.resident) {
+    if (CAUSAL && kt > 0 && bhi < a.resident) {
         constexpr int kWaveBytes = 5 * BK * D * 4;  // Q, dO, O rows + K, V rows
         const unsigned long long slot = (unsigned long long)a.resident * kWaveBytes / kSlotDiv;
         const unsigned long long until = t_start + slot * kt;
@@ -223,7 +206,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         RowLoader ql, gl, ol, kl, vl;
         ql.init(a.q + base, a.ts, S, D);
         gl.init(a.go + base, a.ts, S, D);
-        if (!PROBS) ol.init(a.o + base, a.ts, S, D);
+        ol.init(a.o + base, a.ts, S, D);
         kl.init(a.k + base, a.ts, S, D);
         vl.init(a.v + base, a.ts, S, D);
         constexpr int NK = BK * CPR / 64;
@@ -234,7 +217,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             const int row = kt * BK + f / CPR, cc = f % CPR;
             qv[k] = ql.load(row, cc);
             gv[k] = gl.load(row, cc);
-            if (!PROBS) ov[k] = ol.load(row, cc);
+            ov[k] = ol.load(row, cc);
         }
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) {
@@ -242,23 +225,21 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             vv[s] = vl.load(kj, hf * (D / 8) + s);
         }
         const int ql2 = kt * BK + (lane & (BK - 1));
-        const float lsev = (!PROBS && ql2 < S) ? a.lse[(int64_t)bhi * S + ql2] : 0.f;
+        const float lsev = ql2 < S ? a.lse[(int64_t)bhi * S + ql2] : 0.f;
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
             const int f = lane + 64 * k;
             const int row = kt * BK + f / CPR, cc = f % CPR;
             *reinterpret_cast<floatx4*>(Qr + row * RP + 4 * cc) = qv[k];
             *reinterpret_cast<floatx4*>(Gr + row * RP + 4 * cc) = gv[k];
-            if constexpr (!PROBS) {
-                float d = gv[k][0] * ov[k][0];
+            float d = gv[k][0] * ov[k][0];
 #pragma unroll
-                for (int j = 1; j < 4; ++j) d = fmaf(gv[k][j], ov[k][j], d);
+            for (int j = 1; j < 4; ++j) d = fmaf(gv[k][j], ov[k][j], d);
 #pragma unroll
-                for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
-                if (cc == 0) DV[row] = d;
-            }
+            for (int m = 1; m < CPR; m <<= 1) d += __shfl_xor(d, m);
+            if (cc == 0) DV[row] = d;
         }
-        if (!PROBS && lane < BK) L2[ql2] = ql2 < S ? lsev * kLog2e : kInf;
+        if (lane < BK) L2[ql2] = ql2 < S ? lsev * kLog2e : kInf;
         const float qsc = a.scale * kLog2e;
 #pragma unroll
         for (int s = 0; s < D / 8; ++s) {
@@ -276,118 +257,6 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 
     const bool kedge = kt * BK + BK > S;  // keys past S in this tile
     const int nsteps = CAUSAL ? nt - kt : nt;
-    // the (b, h) slice of the stored probs [S][S] through a buffer resource:
-    // rows past S read as zero
-    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-        PROBS ? const_cast<float*>(a.probs) + (int64_t)bhi * S * S : nullptr, 0, PROBS ? S * S * 4 : 0, kBufferFlags);
-    const int S4 = S * 4;
-
-    if constexpr (PROBS) {
-        // Phase 1: O = P V of whole query tiles, each owned by one wave that
-        // sums its key tiles in ascending order (causally the keys past the
-        // diagonal add exact zeros last, so causal and non-causal agree bit for
-        // bit), then forms the tile's Dq = dO . O and flags it; phase 2's jobs
-        // on a tile wait for that flag.  The product is formed transposed, so V
-        // rows load straight into the A operand and each lane ends with its
-        // query's O for the Dq sum (no LDS round trip).  Causally the light wave of SIMD s
-        // (key tile nt-1-s) owns query tiles s and nt-1-s (s+1 and nt-s
-        // jobs: nt+1 per SIMD), tile s first, the one its heavy partner
-        // starts on; the heavy wave owns none.  Otherwise a wave owns its
-        // key tile's index.
-        // P[query i*32 + c][key j*32 + dq_key(s, h)] for s = 8u + 4w + e
-        auto load_pa = [&](floatx4 (&pa)[4], int j, int i) {
-            const int vo = (i * BK + c) * S4 + (j * BK + 8 * hf) * 4;
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int w = 0; w < 2; ++w) {
-                    const floatx4 v = __builtin_bit_cast(
-                        floatx4, __builtin_amdgcn_raw_buffer_load_b128(pr, vo + (16 * u + 4 * w) * 4, 0, 0));
-                    pa[2 * u + w] = (j * BK + 8 * hf + 16 * u + 4 * w < S) ? v : floatx4{0.f, 0.f, 0.f, 0.f};
-                }
-        };
-        // O^T = V^T P^T: the A operand at step s is V[key j*32 + dq_key(s, h)][dim c],
-        // one coalesced dword per lane (rows past S read as zero)
-        RowLoader vl1;
-        vl1.init(a.v + base, a.ts, S, D);
-        auto load_v = [&](float (&vv)[16], int j) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                vv[e] = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(vl1.rs, (j * BK + dq_key(e, hf)) * vl1.row_bytes + c * 4, 0, 0));
-        };
-        int tiles[2], ntl = 0;
-        if (light) {
-            tiles[0] = kp;
-            tiles[1] = kt;
-            ntl = 2;
-        } else if (!p1_off) {
-            tiles[0] = kt;
-            ntl = 1;
-        }
-        auto tile_of = [&](int n, int& jn) {  // job n -> (tile, key tile jn)
-            const int len0 = CAUSAL ? tiles[0] + 1 : nt;
-            if (n < len0) {
-                jn = n;
-                return tiles[0];
-            }
-            jn = n - len0;
-            return tiles[1];
-        };
-        const int njobs = ntl == 0 ? 0 : (CAUSAL ? tiles[0] + 1 : nt) + (ntl == 2 ? (CAUSAL ? tiles[1] + 1 : nt) : 0);
-        floatx4 pn[4];
-        float vn[16];
-        if (njobs > 0) {
-            int j0;
-            const int i0 = tile_of(0, j0);
-            load_pa(pn, j0, i0);
-            load_v(vn, j0);
-        }
-        floatx16 o;  // register r <-> dim acc_key(r, h), lane <-> query i*32 + c
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[r] = 0.f;
-        for (int n = 0; n < njobs; ++n) {
-            int jn;
-            const int i = tile_of(n, jn);
-            floatx4 pa[4];
-            float vv[16];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) pa[u] = pn[u];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) vv[e] = vn[e];
-            if (n + 1 < njobs) {  // the next job's tiles are requested before this one's products
-                int j1;
-                const int i1 = tile_of(n + 1, j1);
-                load_pa(pn, j1, i1);
-                load_v(vn, j1);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; ++e) o = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[e], pa[e >> 2][e & 3], o, 0, 0, 0);
-            int jl;
-            if (n + 1 == njobs || tile_of(n + 1, jl) != i) {
-                // tile i complete: Dq of query i*32 + c over this half's 16 dims, then the halves summed
-                wait_ge(&staged[i], 1);
-                const float* const g = Gr + (i * BK + c) * RP + 4 * hf;
-                float d = 0.f;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const floatx4 g4 = *reinterpret_cast<const floatx4*>(g + 8 * k);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) d = fmaf(g4[e], o[4 * k + e], d);
-                }
-                d += __shfl_xor(d, 32);
-                if (!hf) DV[i * BK + c] = d;
-                set_flag(&dqready[i], 1);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[r] = 0.f;
-            }
-        }
-    }
-
-    // Stored probs, phase 2: P of query tile i in the accumulator's order.
-    auto load_pk = [&](floatx16& pv, int i) { load_p_tile(pv, pr, i, kj, kval, hf, S); };
-    floatx16 pnext;
-    if constexpr (PROBS) load_pk(pnext, kt);
 
     floatx16 accv, acck;  // dV^T, dK^T (unscaled): register r <-> dim acc_key(r, h), lane <-> key
 #pragma unroll
@@ -404,7 +273,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         return aq;
     };
     // dQ rows through a buffer resource ending at row S-1.  As for the P
-    // loads, only the vector offset is range-checked: whole tiles use a scalar
+    // loads of the stored-probs kernel, only the vector offset is range-checked: whole tiles use a scalar
     // row offset per register, the last tile of a ragged S puts it in the
     // vector offset so the stores of rows past S are dropped.
     const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(
@@ -447,10 +316,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         constexpr bool HP = decltype(has_prev)::value;
         int i = kt + t;
         if (!CAUSAL && i >= nt) i -= nt;
-        if (PROBS)
-            wait_ge(&dqready[i], 1);  // implies tile i staged (its setter waited for that)
-        else if (HP)
-            wait_ge(&staged[i], 1);
+        if (HP) wait_ge(&staged[i], 1);
         const float* qt = Qr + i * BK * RP;
         const float* gt = Gr + i * BK * RP;
         // The chains start from -lse' and -Dq, so they end at S' - lse' and
@@ -458,8 +324,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
         floatx16 sc, dp;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const floatx4 l4 = PROBS ? floatx4{0.f, 0.f, 0.f, 0.f}
-                                     : *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(L2 + i * BK + 8 * g + 4 * hf);
             const floatx4 d4 = *reinterpret_cast<const floatx4*>(DV + i * BK + 8 * g + 4 * hf);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -468,23 +333,14 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
             }
         }
         floatx16 p, ds;
-        if constexpr (PROBS) {
-            // stored probs (a causal forward wrote zeros above the diagonal)
-            p = pnext;
-            if (t + 1 < nsteps) load_pk(pnext, i + 1 < nt ? i + 1 : 0);
-        } else {
-            Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S' - lse', register r <-> query i*32 + acc_key(r, h)
-        }
+        Tiles<D>::dchain(sc, qt, kr2, c, hf);  // S' - lse', register r <-> query i*32 + acc_key(r, h)
         Tiles<D>::dchain(dp, gt, vr, c, hf);  // dP - Dq
         floatx16 aq;
         if constexpr (HP) aq = dq_term();
         // masks: keys past S (last key tile) and, causally, keys past the
         // query on the diagonal job (t == 0)
         const bool edge = HP ? kedge : (kedge || CAUSAL);
-        if constexpr (PROBS) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
-        } else if (edge) {
+        if (edge) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const bool vis = kval && (!CAUSAL || kj <= i * BK + acc_key(r, hf));
@@ -525,8 +381,8 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Stored probs without a causal mask (the reference's drop-in call): every P
-// tile is read from memory once.
+// Stored probs (the reference's contract; its drop-in call has no causal
+// mask): every P tile is read from memory once.
 //
 // At step t every wave works on query tile t against its own key tile j, so
 // the row sums Dq_t = sum_j rowsum(P_tj o dP_tj) complete with one
@@ -539,8 +395,11 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_kernel(BwdArgs a) {
 // in a double-buffered LDS area and, after the next barrier, every wave adds
 // the terms of four of the 32 rows in key-tile order and writes them.  Q and
 // dO tiles stream through a three-slot LDS ring, staged by all threads two
-// steps ahead.  Per step a wave runs 64 MFMAs (dP, dV, dK, dQ) -- the
-// two-phase kernel above runs 80 and reads P twice -- and waits on no flag.
+// steps ahead.  Per step a wave runs 64 MFMAs (dP, dV, dK, dQ; the
+// probs-free kernel above runs 80, as it rebuilds S') and waits on no flag.
+// Causally the wave of key tile j has nothing to add for query tiles t < j
+// (P = 0 there): it skips those steps' products and P reads, keeps its
+// slots of the per-step sums at zero, and joins the barriers.
 // All summation orders are fixed: results are deterministic.
 namespace nc {
 // LDS layout in floats.  The per-wave scratch and the ring come first: DS
@@ -865,13 +724,10 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
 
 }  // namespace bh
 
-// D = 32, S <= 256 and the tiled kernels' layout conditions (bwd_tiled_ok);
-// with stored probs also S % 4 == 0 and 16-byte aligned probs (phase 1 reads
-// them as 16-byte pieces).
-inline bool bh_ok(const BwdArgs& a) {
-    if (a.D != bh::D || a.S < 1 || a.S > bh::MAXS) return false;
-    return !a.probs || (a.S % 4 == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15u) == 0);
-}
+// D = 32, S <= 256 and the tiled kernels' layout conditions (checked by the
+// caller: bwd_tiled_ok).  Stored probs are read as single floats, so there
+// is no condition on S or on the probs' alignment.
+inline bool bh_ok(const BwdArgs& a) { return a.D == bh::D && a.S >= 1 && a.S <= bh::MAXS; }
 
 // Raise a kernel's dynamic-LDS limit once per device (bit d of attr_set).
 inline hipError_t raise_lds_limit(const void* kern, int bytes, std::atomic<unsigned long long>& attr_set) {
@@ -887,11 +743,11 @@ inline hipError_t raise_lds_limit(const void* kern, int bytes, std::atomic<unsig
     return hipSuccess;
 }
 
-template <bool CAUSAL, bool PROBS>
+template <bool CAUSAL>
 hipError_t launch_bh_mode(const BwdArgs& a, hipStream_t s) {
     const int64_t grid = (int64_t)a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
-    auto kern = bh::bwd_bh_kernel<CAUSAL, PROBS>;
+    auto kern = bh::bwd_bh_kernel<CAUSAL>;
     static std::atomic<unsigned long long> attr_set{0};
     hipError_t e = raise_lds_limit(reinterpret_cast<const void*>(kern), bh::kMaxLdsBytes, attr_set);
     if (e != hipSuccess) return e;
@@ -924,7 +780,7 @@ inline hipError_t launch_bh_probs(const BwdArgs& a, hipStream_t s) {
 inline hipError_t launch_bh(const BwdArgs& a, hipStream_t s) {
     // stored probs: the single-read kernel
     if (a.probs) return launch_bh_probs(a, s);
-    return a.causal ? launch_bh_mode<true, false>(a, s) : launch_bh_mode<false, false>(a, s);
+    return a.causal ? launch_bh_mode<true>(a, s) : launch_bh_mode<false>(a, s);
 }
 
 }  // namespace bwd

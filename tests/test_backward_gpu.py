@@ -40,9 +40,9 @@ def _inputs(B, S, E, H, causal=False, seed=0):
 
 
 # D = 32/64/128 MFMA kernels, padded D (7, 16, 48, 96), generic D (160, 256),
-# S below / across / not a multiple of the 32-row tile.  D = 32 with S % 4 == 0
-# and S <= 256 runs the one-workgroup-per-(b, h) kernel (S = 4, 32, 44, 100,
-# 256); other D = 32 shapes the query/key-stationary pair.
+# S below / across / not a multiple of the 32-row tile.  D = 32 with S <= 256
+# runs the one-workgroup-per-(b, h) kernel (S = 1, 4, 7, 32, 44, 64, 100,
+# 256); S = 260 the query/key-stationary pair.
 SHAPES = [
     (1, 1, 32, 1), (2, 7, 64, 2), (1, 33, 128, 2), (2, 64, 256, 2), (1, 100, 96, 2),
     (1, 45, 32, 2), (1, 70, 192, 2), (1, 40, 512, 2), (1, 9, 14, 2), (2, 300, 256, 4),
@@ -86,13 +86,14 @@ def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     """Causal probs: the extended entry point with causal=1 skips tiles above
     the diagonal; the skipped terms are exact zeros, so where both calls run
     the same kernel the result equals the unmasked drop-in bit for bit, and
-    both match the oracle.  The D = 32 cases with S % 4 == 0 run the
-    one-workgroup-per-(b, h) kernels at 1, 2, 3, 5, 7 and 8 key tiles (odd
-    counts leave a middle tile without a SIMD partner): causally the two-phase
-    kernel, unmasked the single-read one, whose Dq sums P o dP instead of
-    dO . (P V) -- there the two agree to the tolerance.  So do the D = 64
-    cases with S <= 256 and fewer (b, h) pairs than CUs: causally the
-    per-(b, h) kernel, unmasked the query-/key-stationary pair."""
+    both match the oracle.  The D = 32 cases run the single-read
+    one-workgroup-per-(b, h) kernel at 1, 2, 3, 5, 7 and 8 key tiles, S = 37
+    ragged by 1 mod 4: causally each wave skips the query tiles before its
+    keys and leaves zeros in its slots of the per-step sums, which adds the
+    same values in the same order, so these are bit-identical too.  The
+    D = 64 cases with S <= 256 and fewer (b, h) pairs than CUs run causally
+    the per-(b, h) kernel, unmasked the query-/key-stationary pair: there the
+    two agree to the tolerance."""
     qkv, go, probs = _inputs(B, S, E, H, causal=True, seed=3)
     want = O.mha_backward(go, qkv, probs, B, S, E, H)
     d_qkv, d_go, d_p = dev_t(qkv), dev_t(go), dev_t(probs)
@@ -103,10 +104,9 @@ def test_causal_backward_skips_only_zero_tiles(dev, B, S, E, H):
     A.launch_multihead_attention_backward(d_go, d_qkv, d_p, g_n, B, S, E, H)
     got = host(g_c)
     assert np.abs(got - want).max() <= tol(want)
-    per_bh = E // H == 32 and S % 4 == 0 and S <= 256
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     split64 = E // H == 64 and S <= 256 and B * H < cus
-    if E // H <= 128 and not per_bh and not split64:  # same MFMA kernels: skipped tiles contribute exact zeros
+    if E // H <= 128 and not split64:  # same MFMA kernels: skipped tiles contribute exact zeros
         assert np.array_equal(got, host(g_n))
     else:
         assert np.abs(got - host(g_n)).max() <= tol(want)
@@ -191,10 +191,11 @@ def test_baseline_config_backward(dev, cfg):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("B,S,E,H", [(2, 44, 64, 2), (3, 100, 128, 4), (2, 236, 64, 2)])
+@pytest.mark.parametrize("B,S,E,H", [(2, 44, 64, 2), (3, 100, 128, 4), (2, 236, 64, 2), (2, 45, 64, 2),
+                                     (1, 7, 32, 1), (2, 255, 64, 2)])
 def test_per_bh_backward_ragged_tail_stays_in_bounds(dev, B, S, E, H, causal):
-    """D = 32 with S % 32 != 0 (S % 4 == 0) runs the one-workgroup-per-(b, h)
-    kernel with a partial last tile, in both modes.  NaN sits directly after
+    """D = 32 with S % 32 != 0 (S % 4 == 0 or not) runs the
+    one-workgroup-per-(b, h) kernel with a partial last tile, in both modes.  NaN sits directly after
     the probs inside the same allocation, so a P load past the last (b, h)'s
     row S-1 would poison dK / dV; rows past S of one (b, h)'s dQ are the next
     batch's rows (or the dK plane), so a dQ store past S would overwrite
