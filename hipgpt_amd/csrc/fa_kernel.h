@@ -99,6 +99,13 @@ struct FaKernel {
     static constexpr bool TRANS_RES = SRT > 0 && sizeof(E) == 4 && TR::KTILE >= QW * 36 && NW <= 2 * NKS;
     static constexpr bool TRANS_OWN = PROBS && CAUSAL && SRT <= 0 && sizeof(E) == 4 && DP >= kTransOwnMinDP;
     static constexpr int LDS_BYTES = BASE_BYTES + (TRANS_OWN ? NW * QW * 36 * 4 : 0);
+    // Without probs, the first stage stages K alone: the first Q K^T waits for
+    // the K rows only, V of that stage is requested once K has landed and is
+    // stored while the first tile's softmax runs (one more workgroup barrier).
+    // Cache-rotated: c1 (fp32, D = 32) 16.86 -> 16.62 us, c3-bf16 31.14 ->
+    // 30.38 us; fp32 D = 64 (c3) 128.3 -> 128.8 us and D = 128 (c4) level, so
+    // those keep the joint first stage.
+    static constexpr bool K_FIRST = !PROBS && (sizeof(E) == 2 || DP == 32);
     // O stores through LDS, one 32-dim block at a time (whole 128-byte row
     // segments per lane group), with a 32 x 36 scratch per storing wave
     // (ks == 0) inside the LDS already allocated: past the merge area when it
@@ -401,6 +408,42 @@ struct FaKernel {
             }
         };
 
+        // K_FIRST: stage 0's online-softmax step in two halves around the
+        // barrier that publishes V -- the scores and the P factors of tile t
+        // with K alone staged, then the P V product.
+        auto first_scores = [&]() -> floatx16 {
+            floatx16 s;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = 0.f;
+            if (ks >= wtiles) return s;
+            s = tile_scores(lds, ks);
+            const float tmax = tile_max(s) * sc;
+            if (__any(tmax > m_run + kLazyMax)) {
+                const float m_new = vmax(m_run, tmax);
+                const float alpha = fast_exp2(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                m_run = m_new;
+            }
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
+                ls += s[r];
+            }
+            l_run += ls;
+            return s;
+        };
+        auto first_pv = [&](const floatx16& p) {
+            if (ks >= wtiles) return;
+            typename TR::VReg vreg;
+            TR::load_v(vreg, vt_of(lds, ks), c, hf);
+            TR::pv(vreg, p, o, c, hf);
+        };
+
         // Stage pipeline: stage i+1 is loaded into registers while stage i is
         // computed, then written to the other LDS buffer.  (Two stages of
         // register prefetch measured no faster at any head dim and cost an
@@ -412,6 +455,30 @@ struct FaKernel {
             constexpr int MODE = decltype(mode_tag)::value;
             constexpr bool WV = MODE != 1;              // the max/sum sweep stages no V
             constexpr bool WK = !(SPILL && MODE == 2);  // nor the spilled probs sweep K
+            if constexpr (MODE == 0 && K_FIRST) {
+                if (nstages > 0) {
+                    st.template load<false, true>(0, tid);
+                    st.template store<false, true>(lds, tid);
+                    st.template load<true, false>(0, tid);
+                }
+                __syncthreads();
+                if (nstages > 0) {
+                    const floatx16 p0 = first_scores();
+                    st.template store<true, false>(lds, tid);
+                    if (nstages > 1) st.template load<true, true>(1, tid);
+                    __syncthreads();
+                    first_pv(p0);
+                    if (nstages > 1) st.template store<true, true>(lds + STAGE_ELEMS, tid);
+                    __syncthreads();
+                }
+                for (int i = 1; i < nstages; ++i) {
+                    if (i + 1 < nstages) st.template load<true, true>(i + 1, tid);
+                    compute(mode_tag, i, mlog, prow, pvec);
+                    if (i + 1 < nstages) st.template store<true, true>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                    __syncthreads();
+                }
+                return;
+            }
             if (nstages > 0) {
                 if (MODE != 2) st.template load<WV, WK>(0, tid);
                 st.template store<WV, WK>(lds, tid);

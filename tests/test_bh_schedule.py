@@ -1,32 +1,28 @@
-"""CPU test of the synchronisation schedule of the one-workgroup-per-(b, h)
-backward (hipgpt_amd/csrc/bwd_bh.h).
+"""CPU test of the synchronisation schedule of the probs-free
+one-workgroup-per-(b, h) backward (bwd_bh_kernel in hipgpt_amd/csrc/bwd_bh.h).
 
 The kernel's waves wait on LDS flags instead of workgroup barriers: a tile's
-"staged" flag, the dQ chain counter of a query tile (contributions in
-descending key-tile order), and with stored probs the per-tile "Dq ready"
-flag.  Every wait is bounded on the device, but a schedule
+"staged" flag and the dQ chain counter of a query tile (contributions in
+descending key-tile order).  Every wait is bounded on the device, but a schedule
 that could block would silently produce wrong gradients, so this test restates
 each wave's sequence of waits and sets (the same key-tile assignment, job
 order and flags as the kernel) and runs them under an event scheduler that
 always picks one runnable wave.  It checks that every schedule completes for
-every tile count 1..8, causal or not, with and without stored probs, under
-both a fixed and randomised choice of the next wave.  A deadlock would leave
-a wave blocked with nothing else runnable.
+every tile count 1..8, causal or not, under both a fixed and randomised
+choice of the next wave.  A deadlock would leave a wave blocked with nothing
+else runnable.
 
 Restated from: key-tile assignment (sr -> kt, SIMD pairs s / nt-1-s), the
 staging flags, job(): step t handles query tile kt + t (mod nt if not
-causal), chain_add(): waits chain[i] >= t and sets t + 1 unless last; PROBS:
-phase 1 gives query tile i's O to one wave (causally the light wave of the
-SIMD pair owns the partner's tile, then its own; the heavy wave none; else a
-wave owns its key tile's index), which waits staged[i] once the tile's O is
-summed and sets dqready[i]; phase-2 jobs wait dqready[i].
+causal), waiting staged[i] from the second job on; chain_add(): waits
+chain[i] >= t and sets t + 1 unless last.
 """
 import random
 
 import pytest
 
 
-def wave_programs(nt, causal, probs):
+def wave_programs(nt, causal):
     """Per wave, a list of ("wait", flag, tile, value) / ("set", flag, tile, value) ops."""
     waves = []
     for sr in range(8):
@@ -36,9 +32,6 @@ def wave_programs(nt, causal, probs):
             kt = (nt - 1 - s2 if nt - 1 - s2 > s2 else -1) if (sr & 1) else s2
         if kt < 0:
             continue
-        light = probs and causal and (sr & 1)
-        p1_off = probs and causal and not (sr & 1) and nt - 1 - s2 > s2
-        kp = s2
         ops = [("set", "staged", kt, 1)]
         nsteps = nt - kt if causal else nt
 
@@ -46,18 +39,11 @@ def wave_programs(nt, causal, probs):
             i = k + t
             return i - nt if (not causal and i >= nt) else i
 
-        if probs:  # phase 1: no waits until a tile's O is summed in registers
-            owned = [kp, kt] if light else ([] if p1_off else [kt])
-            for i in owned:
-                ops.append(("wait", "staged", i, 1))
-                ops.append(("set", "dqready", i, 1))
-        # phase 2 (or the only phase): job t, its dQ term added one job later
+        # job t, its dQ term added one job later
         prev = None
         for t in range(nsteps):
             i = tile(kt, t)
-            if probs:
-                ops.append(("wait", "dqready", i, 1))
-            elif t > 0:
+            if t > 0:
                 ops.append(("wait", "staged", i, 1))
             if prev is not None:
                 ops += chain_ops(*prev, nt, causal)
@@ -96,7 +82,7 @@ def run(waves, nt, rng=None):
         w = rng.choice(runnable) if rng else runnable[0]
         kind, flag, i, v = waves[w][1][pos[w]]
         if kind == "set":
-            assert flags.get((flag, i), 0) == v - 1 or flag in ("staged", "dqready"), (flag, i, v)
+            assert flags.get((flag, i), 0) == v - 1 or flag == "staged", (flag, i, v)
             flags[(flag, i)] = v
         elif kind == "done":
             finished_dq.append(i)
@@ -105,15 +91,11 @@ def run(waves, nt, rng=None):
     return blocked, sorted(finished_dq)
 
 
-@pytest.mark.parametrize("probs", [False, True])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("nt", range(1, 9))
-def test_every_wait_ends(nt, causal, probs):
-    waves = wave_programs(nt, causal, probs)
+def test_every_wait_ends(nt, causal):
+    waves = wave_programs(nt, causal)
     assert sorted(kt for kt, _ in waves) == list(range(nt))  # each key tile owned once
-    if probs:  # each query tile's Dq formed once
-        sets = [i for _, ops in waves for kind, flag, i, _ in ops if kind == "set" and flag == "dqready"]
-        assert sorted(sets) == list(range(nt))
     for rng in [None] + [random.Random(seed) for seed in range(20)]:
         blocked, done = run(waves, nt, rng)
         assert not blocked, f"waves of key tiles {blocked} never finish"
@@ -124,7 +106,7 @@ def test_chain_order_is_descending_key_tiles():
     """Causal: query tile i receives its dQ terms from key tiles i, i-1, ..., 0
     in that order (the fixed summation order that makes dQ deterministic)."""
     nt = 8
-    waves = wave_programs(nt, True, False)
+    waves = wave_programs(nt, True)
     owner = {}
     for kt, ops in waves:
         for kind, flag, i, v in ops:
