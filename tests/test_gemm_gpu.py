@@ -132,14 +132,13 @@ def test_strided_operands_and_column_planes(dev):
     check_fp32(got, An, Wn, bn, want)
 
 
-def test_baseline_layer_shapes_sampled_rows(dev):
+def test_baseline_layer_shapes_every_row(dev):
     """The c1 layer's projections (T = 32*256 tokens, E = 256): QKV
     [8192, 256] x [256, 768] and out-projection [8192, 256] x [256, 256],
-    checked on a seeded sample of 256 rows (the oracle is scalar)."""
+    every output element checked (the scalar C oracle takes ~1 s here)."""
     T, E = 8192, 256
     for N_out in (3 * E, E):
         A, B, bias = operands(0x51 + N_out, T, E, N_out)
         got = host(P.gemm_bias(dev_t(A), dev_t(B), dev_t(bias)))
-        rows = np.random.default_rng(N_out).choice(T, size=256, replace=False)
-        want = O.matmul_add_bias(A[rows], B, bias, 256, E, N_out)
-        check_fp32(got[rows], A[rows], B, bias, want)
+        want = O.matmul_add_bias(A, B, bias, T, E, N_out)
+        check_fp32(got, A, B, bias, want)
