@@ -106,6 +106,12 @@ struct FaKernel {
     // 30.38 us; fp32 D = 64 (c3) 128.3 -> 128.8 us and D = 128 (c4) level, so
     // those keep the joint first stage.
     static constexpr bool K_FIRST = !PROBS && (sizeof(E) == 2 || DP == 32);
+    // Score-resident sweeps over at most two stages at D = 32 (the small
+    // problems' 1 x 4 workgroups: HipGPT's generation call): K and V of both
+    // stages are requested at once into the two stage buffers, so neither
+    // sweep waits on a load after the first (each stage's loads were
+    // otherwise requested one stage, ~0.5 us of compute, before use).
+    static constexpr bool LOAD_ALL = SRT == 2 && DP == 32;
     // O stores through LDS, one 32-dim block at a time (whole 128-byte row
     // segments per lane group), with a 32 x 36 scratch per storing wave
     // (ks == 0) inside the LDS already allocated: past the merge area when it
@@ -510,8 +516,60 @@ struct FaKernel {
         // Score-resident probs sweeps (SRT > 0).  Stage I holds tile I*NKS + ks
         // of this wave; sres[I] keeps its masked scores between the sweeps.
         floatx16 sres[SRT > 0 ? SRT : 1];
+        // One tile of a score-resident sweep: max/sum (first) or probs + P V (second).
+        auto res_tile = [&](auto second_tag, auto ic, const E* cur, float mlog, float* prow, bool pvec) {
+            constexpr bool SECOND = decltype(second_tag)::value;
+            constexpr int I = decltype(ic)::value;
+            const int t = I * NKS + ks;
+            if (t >= wtiles) return;
+            if (!SECOND) {
+                const floatx16 sv = tile_scores(cur, t);
+                sres[I] = sv;
+                const float m_new = vmax(m_run, tile_max(sv) * sc);
+                float ls = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(sv[r], sc, -m_new));
+                l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
+                m_run = m_new;
+            } else {
+                typename TR::VReg vreg;
+                TR::load_v(vreg, vt_of(cur, t), c, hf);
+                floatx16 p = sres[I];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -mlog));
+                if constexpr (TRANS_RES) {
+                    float* const X =
+                        reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS + (wave % NKS) * TR::KTILE);
+                    store_t(X, prow - (int64_t)c * Sk, p, t * BK, pvec);
+                } else {
+                    if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
+                }
+                TR::pv(vreg, p, o, c, hf);
+            }
+        };
         auto sweep_res = [&](auto second_tag, float mlog, float* prow, bool pvec) {
             constexpr bool SECOND = decltype(second_tag)::value;  // false: max/sum (K), true: probs + PV (V)
+            if constexpr (LOAD_ALL) {
+                // both stages requested at once and kept in the two buffers
+                if (!SECOND) {
+                    Stager st2 = st;
+                    if (nstages > 0) st.template load<true, true>(0, tid);
+                    if (nstages > 1) st2.template load<true, true>(1, tid);
+                    if (nstages > 0) st.template store<true, true>(lds, tid);
+                    if (nstages > 1) st2.template store<true, true>(lds + STAGE_ELEMS, tid);
+                    __syncthreads();
+                }
+                static_for(
+                    [&](auto ic) {
+                        constexpr int I = decltype(ic)::value;
+                        if (I < nstages) res_tile(second_tag, ic, lds + I * STAGE_ELEMS, mlog, prow, pvec);
+                    },
+                    std::make_integer_sequence<int, SRT>{});
+                // the merge slots (after the first sweep) and the O merge
+                // (after the second) reuse the K half of buffer 0
+                __syncthreads();
+                return;
+            }
             if (nstages > 0) {
                 // the probs sweep's first V stage was requested in the max/sum sweep's first stage
                 if (!SECOND) st.template load<false, true>(0, tid);
@@ -524,34 +582,7 @@ struct FaKernel {
                     if (I < nstages) {
                         if (I + 1 < nstages) st.template load<SECOND, !SECOND>(I + 1, tid);
                         if (!SECOND && I == 0) st.template load<true, false>(0, tid);  // V of the probs sweep's first stage
-                        const E* cur = lds + (I & 1) * STAGE_ELEMS;
-                        const int t = I * NKS + ks;
-                        if (t < wtiles) {
-                            if (!SECOND) {
-                                const floatx16 sv = tile_scores(cur, t);
-                                sres[I] = sv;
-                                const float m_new = vmax(m_run, tile_max(sv) * sc);
-                                float ls = 0.f;
-#pragma unroll
-                                for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(sv[r], sc, -m_new));
-                                l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
-                                m_run = m_new;
-                            } else {
-                                typename TR::VReg vreg;
-                                TR::load_v(vreg, vt_of(cur, t), c, hf);
-                                floatx16 p = sres[I];
-#pragma unroll
-                                for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(p[r], sc, -mlog));
-                                if constexpr (TRANS_RES) {
-                                    float* const X = reinterpret_cast<float*>(lds + (wave / NKS) * STAGE_ELEMS +
-                                                                              (wave % NKS) * TR::KTILE);
-                                    store_t(X, prow - (int64_t)c * Sk, p, t * BK, pvec);
-                                } else {
-                                    if (qi < Sq) store_probs_tile(prow, p, t * BK, hf, Sk, pvec);
-                                }
-                                TR::pv(vreg, p, o, c, hf);
-                            }
-                        }
+                        res_tile(second_tag, ic, lds + (I & 1) * STAGE_ELEMS, mlog, prow, pvec);
                         if (I + 1 < nstages)
                             st.template store<SECOND, !SECOND>(lds + ((I + 1) & 1) * STAGE_ELEMS, tid);
                         __syncthreads();
