@@ -232,7 +232,7 @@ struct WideKV {
     static constexpr int LDS_FLOATS = NBUF * STAGE + XCH;
     static_assert(STAGE % 4 == 0, "16-byte aligned stage buffers");
 
-    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int nkb, int bh, int rank) {
+    __device__ __forceinline__ static void run(const BwdArgs& a, float* lds, int bh, int rank) {
         const int tid = threadIdx.x, lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int c = lane & 31, hf = lane >> 5;
@@ -400,11 +400,11 @@ __global__ __launch_bounds__(NQB* DH * 64) void bwd_wide_q_kernel(BwdArgs a, int
 }
 
 template <int DP, int NKB, int DH, int NBUF, bool CAUSAL, bool RECOMP>
-__global__ __launch_bounds__(NKB* DH * 64) void bwd_wide_kv_kernel(BwdArgs a, int nkb) {
+__global__ __launch_bounds__(NKB* DH * 64) void bwd_wide_kv_kernel(BwdArgs a) {
     using K = WideKV<DP, NKB, DH, NBUF, CAUSAL, RECOMP>;
     __shared__ __attribute__((aligned(16))) float lds[K::LDS_FLOATS];
     const int BH = a.B * a.H;
-    K::run(a, lds, nkb, blockIdx.x % BH, blockIdx.x / BH);
+    K::run(a, lds, blockIdx.x % BH, blockIdx.x / BH);
 }
 
 // Both kernels of one problem (the second reads the first's Dq).  Blocks
@@ -421,7 +421,7 @@ hipError_t launch_wide_mode(const BwdArgs& a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_wide_kv_kernel<DP, NB, DH, NBUF, CAUSAL, RECOMP>), dim3((unsigned)g), dim3(NB * DH * 64),
-                       0, s, a, nb);
+                       0, s, a);
     return hipGetLastError();
 }
 

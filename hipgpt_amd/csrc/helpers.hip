@@ -436,7 +436,7 @@ hipError_t grid_1d(int64_t n, unsigned& blocks) {
 }
 
 template <int DP>
-void launch_sdp_tiles(const float* Q, const float* K, float* scores, int B, int S, float inv, hipStream_t s,
+void launch_sdp_tiles(const float* Q, const float* K, float* scores, int S, float inv, hipStream_t s,
                       unsigned blocks, int n_qg, int n_kc, int kc_tiles, int vec_store) {
     hipLaunchKernelGGL(sdp_tiles_kernel<DP>, dim3(blocks), dim3(256), 0, s, Q, K, scores, S, inv, n_qg, n_kc, kc_tiles,
                        vec_store);
@@ -465,9 +465,9 @@ hipError_t launch_sdp(const float* Q, const float* K, float* scores, int B, int 
         unsigned blocks;
         const hipError_t e = grid_1d((int64_t)B * n_qg * n_kc, blocks);
         if (e != hipSuccess) return e;
-        if (D == 32) launch_sdp_tiles<32>(Q, K, scores, B, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
-        if (D == 64) launch_sdp_tiles<64>(Q, K, scores, B, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
-        if (D == 128) launch_sdp_tiles<128>(Q, K, scores, B, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
+        if (D == 32) launch_sdp_tiles<32>(Q, K, scores, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
+        if (D == 64) launch_sdp_tiles<64>(Q, K, scores, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
+        if (D == 128) launch_sdp_tiles<128>(Q, K, scores, S, inv, s, blocks, n_qg, n_kc, kc_tiles, vec_store);
         return hipGetLastError();
     }
     unsigned blocks;
