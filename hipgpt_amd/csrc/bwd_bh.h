@@ -616,11 +616,14 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     // false) forms dnx = dP of tile t+1 and its partial row sums, and loads P
     // of tile t+2 into pc (the last tile again past the end).  Steps
     // alternate the buffers' roles, so no registers are copied.
-    auto step = [&](auto last_tag, auto par_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dc, floatx16& dnx) {
+    auto step = [&](auto last_tag, auto par_tag, auto early_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dc,
+                    floatx16& dnx) {
         constexpr bool LAST = decltype(last_tag)::value;
         constexpr int PAR = decltype(par_tag)::value;
+        constexpr bool EARLY = decltype(early_tag)::value;
         const float* qt = slot(t);
         const float* gt = qt + nc::TILE;
+        if constexpr (EARLY && !LAST) dnx = dp_tile(slot(t + 1) + nc::TILE);
         // Dq of query tile t (lane: query c): the partials in key-tile order
         // (zeros past the last key tile), kept in the scratch's padding for
         // the register-order reads below
@@ -654,7 +657,7 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
             aq = __builtin_amdgcn_mfma_f32_32x32x2f32(X[dq_key(s, hf) * XP + c], kq[s], aq, 0, 0, 0);
         if constexpr (!LAST) {
             // the next query tile: dP, the partial row sums, and P two tiles ahead
-            dnx = dp_tile(slot(t + 1) + nc::TILE);
+            if constexpr (!EARLY) dnx = dp_tile(slot(t + 1) + nc::TILE);
             load_p_tile(pc, pr, t + 2 < nt ? t + 2 : nt - 1, kj, kval, hf, S);
             partial(std::integral_constant<int, 1 - PAR>{}, pnx, dnx);
         }
@@ -681,9 +684,16 @@ __global__ __launch_bounds__(NW * 64) void bwd_bh_probs_kernel(BwdArgs a) {
     };
     auto run_step = [&](auto last_tag, auto par_tag, int t, floatx16& pc, floatx16& pnx, floatx16& dc, floatx16& dnx) {
         if (!active) return;
-        if (!CAUSAL || t >= wave)
-            step(last_tag, par_tag, t, pc, pnx, dc, dnx);
-        else
+        if (!CAUSAL || t >= wave) {
+            // unmasked: the waves of the upper half form the next tile's dP
+            // first, so each SIMD's two waves (w, w + 4) reach their
+            // matrix-free stretches at different times (c1 drop-in 50.5 ->
+            // 49.9 us; the causal instance would exceed its registers)
+            if (!CAUSAL && wave >= NW / 2)
+                step(last_tag, par_tag, std::integral_constant<bool, !CAUSAL>{}, t, pc, pnx, dc, dnx);
+            else
+                step(last_tag, par_tag, std::false_type{}, t, pc, pnx, dc, dnx);
+        } else
             idle_step(par_tag, t, pc, pnx, dnx);  // t < wave <= nt - 1: never the last step
     };
     // Every wave after its step on tile t: the dQ rows of tile t-1, the ring,
