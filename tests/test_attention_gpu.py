@@ -74,12 +74,14 @@ def test_planar_causal_matches_oracle(dev, B, S, E, H, causal, with_probs):
 # 128..256 keys and few query tiles (D <= 32: at most 128, D = 64: at most
 # 512): the launcher splits each query sub-block's keys over 4 waves
 # (HipGPT's generation call, B = 1, H = 8, S = 256, at D = 32 and 64, is one
-# such shape).  Padded D (16, 24, 48), ragged S, both masks, probs on and off.
+# such shape).  Padded D (16, 24, 48), ragged S, both masks, probs on and off;
+# at D = 32 with probs a wave's keys span one stage (S = 128) or two (S = 129 ..
+# 256), which are loaded together.
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("with_probs", [True, False])
 @pytest.mark.parametrize("B,S,E,H", [(1, 256, 256, 8), (2, 129, 64, 2), (1, 200, 96, 4), (2, 128, 32, 2),
                                      (1, 250, 48, 2), (1, 256, 512, 8), (2, 150, 128, 2), (3, 130, 192, 4),
-                                     (8, 256, 512, 8)])
+                                     (8, 256, 512, 8), (1, 128, 256, 8), (3, 160, 96, 3), (2, 255, 64, 2)])
 def test_small_grid_key_split_matches_oracle(dev, B, S, E, H, causal, with_probs):
     qkv = O.seeded_planar(S * 17 + E + B, B, S, E)
     want_o, want_p = O.launch_multihead_attention(qkv, B, S, E, H, causal=causal, want_probs=True)
