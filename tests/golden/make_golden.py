@@ -7,7 +7,8 @@ stores the reference's O and P.  The shapes cover both reference kernels:
 flash_attention_kernel<32|64> (D in {32, 64}, S <= 512) and the fallback
 (other D, or S > 512).  Inputs are not stored: the seed and a checksum are.
 
-Usage (GPU box, repo root):  python tests/golden/make_golden.py OUTDIR
+Usage (GPU box, repo root):  python tests/golden/make_golden.py [OUTDIR]
+(OUTDIR defaults to this directory, where the committed fixtures live.)
 """
 import os
 import sys
@@ -52,4 +53,4 @@ def main(outdir):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else os.path.join(ROOT, "gpurun_out", "golden"))
+    main(sys.argv[1] if len(sys.argv) > 1 else os.path.dirname(os.path.abspath(__file__)))
