@@ -30,6 +30,15 @@ __device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is.
 // O / l rescale is skipped on most tiles; exponentiated scores are then at
 // most 2^kLazyMax, far from fp32 overflow, and the final O / l is unchanged.
 constexpr float kLazyMax = 8.0f;
+// After a row's first tile the running max can also be checked without
+// forming the tile's max: exponentiate against the running max and test the
+// lane's sum of the 16 exponentials against 2^kLazyMax.  No exponential
+// exceeds 2^kLazyMax when the sum does not (all are >= 0), which is exactly
+// when the max test keeps the running max; a larger sum sends the tile back
+// through the max test (scores recomputed), so the results are the same bit
+// for bit and the common tile saves the max reduction (8 v_maximum3, a lane
+// exchange, a compare).
+constexpr float kLazySum = 256.0f;  // 2^kLazyMax
 
 // SIMD of the calling wave (HW_ID.SIMD_ID, bits [5:4]).
 __device__ __forceinline__ int wave_simd() { return (__builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11))) & 3; }

@@ -106,6 +106,13 @@ struct FaKernel {
     // 30.38 us; fp32 D = 64 (c3) 128.3 -> 128.8 us and D = 128 (c4) level, so
     // those keep the joint first stage.
     static constexpr bool K_FIRST = !PROBS && (sizeof(E) == 2 || DP == 32);
+    // Causal online-softmax sweeps with 16-byte loads test the running max
+    // through the exponentials' sum (kLazySum) after each wave's first tile.
+    // Cache-rotated, two interleaved repetitions: c1 16.63 -> 16.56 us, c3
+    // 127.9 -> 127.4, c3-bf16 29.56 -> 29.24, c4 580.2 -> 576.7; results
+    // unchanged bit for bit.  The non-causal D = 32 instance and the
+    // guarded-load D = 128 ones spill registers with it and keep the max test.
+    static constexpr bool SUM_CHECK = CAUSAL && VEC;
     // Score-resident sweeps over at most two stages at D = 32 (the small
     // problems' 1 x 4 workgroups: HipGPT's generation call): K and V of both
     // stages are requested at once into the two stage buffers, so neither
@@ -370,29 +377,50 @@ struct FaKernel {
             }
             typename TR::VReg vreg;
             if (MODE != 1) TR::load_v(vreg, vt_of(cur, t), c, hf);  // in flight during the softmax
-            if (MODE == 0) {
+            if constexpr (MODE == 0) {
                 // lazy rescale: raise the running max only when a row's tile
                 // max exceeds it by more than kLazyMax
-                const float tmax = tile_max(s) * sc;
-                if (__any(tmax > m_run + kLazyMax)) {
-                    const float m_new = vmax(m_run, tmax);
-                    const float alpha = fast_exp2(m_run - m_new);
-                    l_run *= alpha;
+                auto lazy_exp = [&](floatx16& sv) -> float {
+                    const float tmax = tile_max(sv) * sc;
+                    if (__any(tmax > m_run + kLazyMax)) {
+                        const float m_new = vmax(m_run, tmax);
+                        const float alpha = fast_exp2(m_run - m_new);
+                        l_run *= alpha;
 #pragma unroll
-                    for (int db = 0; db < NDB; ++db)
+                        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-                    m_run = m_new;
-                }
-                float ls = 0.f;
+                            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                        m_run = m_new;
+                    }
+                    float lsum = 0.f;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
-                    ls += s[r];
+                    for (int r = 0; r < 16; ++r) {
+                        sv[r] = fast_exp2(fmaf(sv[r], sc, -m_run));
+                        lsum += sv[r];
+                    }
+                    return lsum;
+                };
+                float ls;
+                if (!SUM_CHECK || i == 0) {  // stage 0 holds every wave's first tile
+                    ls = lazy_exp(s);
+                } else {
+                    // the sum test of kLazySum; the max test only when it fails,
+                    // with the scores recomputed from the staged K tile
+                    ls = 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
+                        ls += s[r];
+                    }
+                    if (__any(ls > kLazySum)) {
+                        asm volatile("" ::: "memory");  // re-read K: no copy of the first product stays live
+                        s = tile_scores(cur, t);
+                        ls = lazy_exp(s);
+                    }
                 }
                 l_run += ls;  // this lane half's partial; the halves are summed after the sweep
                 TR::pv(vreg, s, o, c, hf);
-            } else if (MODE == 1) {
+            } else if constexpr (MODE == 1) {
                 if constexpr (SPILL && TRANS_OWN)
                     store_t(Xown, prow - (int64_t)c * Sk, s, t * BK, pvec);
                 else if (SPILL && qi < Sq)
