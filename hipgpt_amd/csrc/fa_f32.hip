@@ -174,11 +174,17 @@ int fa_f32_padded_dim(int D) {
     return 0;
 }
 
-// Short sequences at DP = 64 (all K/V tiles of a (b, h) fit one workgroup's
-// LDS) run the resident kernel: 8 waves = 256 queries per workgroup.  At
-// DP = 32 the streaming kernel measured faster (17.2 against 17.5 us at c1:
-// its four waves per SIMD hide the short tiles' softmax better).
-constexpr int kResidentMaxSq = 256;
+// Probs rows of 193 to 256 keys at DP = 64 (all K/V tiles of a (b, h) fit one
+// workgroup's LDS) run the resident kernel: 8 waves = 256 queries per
+// workgroup, the scores kept between the sweeps.  Cache-rotated, B*H = 256:
+// S = 256 with probs 40.6 (causal) / 55.3 us (drop-in) against 50.7 / 65.0
+// for the streaming kernel.  Everything else streams: without probs the
+// streaming kernel measured 31.2 against 32.7 us at S = 256 (causal; 44.3
+// against 45.4 non-causal), 23.4 against 33.4 at S = 128 and 40.8 against
+// 55.8 at S = 192; with probs at S = 128 / 192, 35.6 / 55.6 against 41.9 /
+// 68.5 us causal and level / 73.1 against 75.4 non-causal.  At DP = 32 the
+// streaming kernel measured faster at every S (17.2 against 17.5 us at c1).
+constexpr int kResidentMinSq = 193, kResidentMaxSq = 256;
 
 // Small D <= 32 problems (at most 128 query tiles of 32 rows in all, 128 to
 // 256 keys -- HipGPT's generation call, B = 1, H = 8, S = 256, is 64 tiles):
@@ -221,12 +227,12 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
                           : fa::launch_fa<T6, NQ, NK, false, false, true>(a, stream);
         }
     }
-    // one workgroup per (b, h) and CU: only when the (b, h) pairs fill the
-    // device (at B*H = 128, S = 256 the streaming kernel measured 38.8 against
-    // 53.7 us for the drop-in, 24.3 against 31.2 causal); the resident kernel
+    // one workgroup per (b, h) and CU: only with probs and when the (b, h)
+    // pairs fill the device (at B*H = 128, S = 256 the streaming kernel
+    // measured 38.8 against 53.7 us for the drop-in); the resident kernel
     // writes no lse
-    if (vec && a.Sq <= kResidentMaxSq && !a.lse && a.D == 64 && (int64_t)a.B * a.H >= device_cus() &&
-        fa::resident_lds_bytes<F32Traits<64, true>, 8>(a) != 0)
+    if (vec && probs && a.Sq >= kResidentMinSq && a.Sq <= kResidentMaxSq && !a.lse && a.D == 64 &&
+        (int64_t)a.B * a.H >= device_cus() && fa::resident_lds_bytes<F32Traits<64, true>, 8>(a) != 0)
         return fa::launch_resident<F32Traits<64, true>, 8, 4>(a, causal, stream);
     switch (fa_f32_padded_dim(a.D)) {
         case 32: return launch_dp<32, 2, 2>(a, causal, probs, vec, stream);

@@ -8,7 +8,8 @@ These inputs make the online softmax move its running max far and often
 and the resident-K/V kernel with scores far from the unit-variance range.
 
 Shapes: c1 (D=32, streaming kernel, scores kept in registers with probs),
-c2 (D=64, S=256, B*H=256: the resident-K/V kernel), c3 (D=64, S=1024:
+c2 (D=64, S=256, B*H=256: the resident-K/V kernel with probs, the streaming
+kernel without), c3 (D=64, S=1024:
 streaming 4x2, Q.K^T recomputed with probs) and c4's head shape at B=1
 (D=128, S=2048: probs rows spilled and read back).
 
