@@ -309,7 +309,8 @@ hipError_t launch_dp(const BwdArgs& a, hipStream_t s) {
 // Workgroup shapes of the tiled kernels: query-stationary NQS x NKS,
 // key-stationary NKB x NQS.  4 x 1 for both was best or within 3% of the
 // best of nine shapes on MI355X for the c1 causal, c1 non-causal and c2
-// causal backward.
+// causal backward; with stored probs, launch_tiled_probs also takes 4 x 2
+// where the grid fills the device's slots better with it.
 constexpr int kBwdQNqs = 4, kBwdQNks = 1, kBwdKvNkb = 4, kBwdKvNqs = 1;
 
 hipError_t bwd_wait_expired(unsigned int* count, bool clear) { return wait_expired_take(count, clear); }
@@ -356,6 +357,7 @@ hipError_t launch_attn_bwd(const BwdArgs& a, hipStream_t s) {
     if (bwd_tiled_ok(a)) {
         if (bh_enough(a) && bwd::bh_ok(a)) return bwd::launch_bh(a, s);
         if (bh_enough(a) && (bwd::bh_probs64_ok(a) || bwd::bh_lse64_ok(a))) return bwd::launch_bh64(a, s);
+        if (a.probs) return a.D == 32 ? bwd::launch_tiled_probs<32>(a, s) : bwd::launch_tiled_probs<64>(a, s);
         if (a.D == 32)
             return bwd::launch_tiled<32, kBwdQNqs, kBwdQNks, kBwdKvNkb, kBwdKvNqs>(a, s);
         return bwd::launch_tiled<64, kBwdQNqs, kBwdQNks, kBwdKvNkb, kBwdKvNqs>(a, s);

@@ -671,6 +671,40 @@ hipError_t launch_tiled_mode(const BwdArgs& a, hipStream_t s) {
     }
 }
 
+// Stored probs: 4 x 1 workgroups, or 4 x 2 -- each query-stationary
+// workgroup's keys and each key-stationary workgroup's queries split over two
+// more waves, so a workgroup takes about half as long at half as many resident
+// slots (one 8-wave workgroup per CU instead of two 4-wave ones; the same
+// 128-row blocks, so the same grid).  The split pays when the 4 x 1 grid
+// would end on a partly filled round: without a causal mask, when
+// ceil(G / S2) / 2 (+10% for the wider workgroup) is below ceil(G / S1);
+// causally (longest blocks first), when the whole grid fits one 4 x 2 round.
+// Cache-rotated, D = 64: the HipGPT drop-in at B8 H12 S1024 (G = 768) 868 ->
+// 737 us, B8 H8 S512 non-causal (G = 256) 148 -> 135, causal 142 -> 131;
+// kept 4 x 1: non-causal B2 H12 S2048 (G = 384: 856 against 940 us), D = 32
+// B8 H8 S1024 (G = 512: 259 against 285), causal B8 H12 S1024 (G = 768: 410
+// against 436).  The probs-free pair keeps 4 x 1 (449 against 482 us at B8
+// H12 S1024 causal).
+template <int DP>
+hipError_t launch_tiled_probs(const BwdArgs& a, hipStream_t s) {
+    static ResidentSlots c1[2], c2[2];
+    const int ci = a.causal ? 1 : 0;
+    const void* k1 = a.causal ? reinterpret_cast<const void*>(bwd_q_kernel<DP, 4, 1, true, false>)
+                              : reinterpret_cast<const void*>(bwd_q_kernel<DP, 4, 1, false, false>);
+    const void* k2 = a.causal ? reinterpret_cast<const void*>(bwd_q_kernel<DP, 4, 2, true, false>)
+                              : reinterpret_cast<const void*>(bwd_q_kernel<DP, 4, 2, false, false>);
+    const int64_t S1 = c1[ci].get(k1, 4 * 64, 0), S2 = c2[ci].get(k2, 8 * 64, 0);
+    const int64_t G = (int64_t)((a.S + 4 * BK - 1) / (4 * BK)) * a.B * a.H;
+    bool split = false;
+    if (S1 > 0 && S2 > 0)
+        split = a.causal ? G <= S2 : 11 * ((G + S2 - 1) / S2) < 20 * ((G + S1 - 1) / S1);
+    if (split)
+        return a.causal ? launch_tiled_mode<DP, 4, 2, 4, 2, true, false>(a, s)
+                        : launch_tiled_mode<DP, 4, 2, 4, 2, false, false>(a, s);
+    return a.causal ? launch_tiled_mode<DP, 4, 1, 4, 1, true, false>(a, s)
+                    : launch_tiled_mode<DP, 4, 1, 4, 1, false, false>(a, s);
+}
+
 template <int DP, int QNQS, int QNKS, int KNKB, int KNQS>
 hipError_t launch_tiled(const BwdArgs& a, hipStream_t s) {
     const bool recomp = a.probs == nullptr;
