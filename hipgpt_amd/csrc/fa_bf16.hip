@@ -130,14 +130,34 @@ struct B16Traits {
     }
 };
 
-// Workgroup shape: 4 query sub-blocks share each K/V stage (bf16 tiles are
-// short on the matrix cores, so the stage's loads, LDS stores and barrier
-// are amortised over more work); 4 x 2 measured best of 2x2, 4x1, 4x2, 2x4, 8x1.
-constexpr int kNqs = 4, kNks = 2;
+// Workgroup shape: 4 query sub-blocks (128 queries) share each K/V stage
+// (bf16 tiles are short on the matrix cores, so the stage's loads, LDS
+// stores and barrier are amortised over more work), each sub-block's keys
+// split over 2 waves (4 x 2) or not (4 x 1).  A 4 x 1 workgroup takes half
+// the CU, so the device holds twice as many, and where the 4 x 2 grid would
+// need more than one round of resident workgroups the smaller workgroups
+// fill the device better: without a causal mask when the grid exceeds the
+// 4 x 2 slots, with one when it exceeds even the 4 x 1 slots (a causal grid
+// that fits them at once measured slower: its longest rows, unsplit, set the
+// end).  Cache-rotated, us, 4 x 2 -> 4 x 1 (G workgroups): non-causal
+// B8 H12 S1024 D64 (G 768 against 512 4 x 2 slots) 47.5 -> 40.1, B4 H16
+// S2048 D128 (G 1024 / 256) 209.8 -> 171.0; causal B4 H16 S2048 D128
+// (G 1024 against 512 4 x 1 slots) 127.0 -> 110.1, B16 H12 S1024 D64
+// (G 1536 / 1024) 58.9 -> 50.5.  Kept at 4 x 2: causal c3 (G 768 / 1024)
+// 29.6 against 40.3, B4 H16 S2048 D64 (G 1024 / 1024) 56.9 / 72.1, B1 and
+// B2 H12 S1024 D64 23.5 / 33.9 and 24.2 / 35.6, B32 H8 S256 D32 / D64
+// 12.3 / 13.1 and 12.8 / 14.5; non-causal B32 H8 S256 D64 (G 512 / 512)
+// 13.7 / 13.8.  2 x 1 and 8 x 1 measured between the two or slower.
+constexpr int kNqs = 4;
 
 template <int D>
 hipError_t launch_d(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
-    return fa::launch_fa_flags<B16Traits<D>, kNqs, kNks, true>(a, causal, probs, s);
+    using T = B16Traits<D>;
+    const int64_t grid = (int64_t)((a.Sq + kNqs * 32 - 1) / (kNqs * 32)) * a.B * a.H;
+    const int slots = causal ? fa::fa_resident_slots<T, kNqs, 1, true, true>()
+                             : fa::fa_resident_slots<T, kNqs, 2, false, true>();
+    if (slots > 0 && grid > slots) return fa::launch_fa_flags<T, kNqs, 1, true>(a, causal, probs, s);
+    return fa::launch_fa_flags<T, kNqs, 2, true>(a, causal, probs, s);
 }
 
 }  // namespace

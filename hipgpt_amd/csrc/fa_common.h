@@ -39,6 +39,9 @@ constexpr float kLazyMax = 8.0f;
 // for bit and the common tile saves the max reduction (8 v_maximum3, a lane
 // exchange, a compare).
 constexpr float kLazySum = 256.0f;  // 2^kLazyMax
+// Start of a sum of exponentials: -0 is the additive identity (x + -0 == x
+// for every x), so the first add folds away; from +0 it stays an instruction.
+constexpr float kSumInit = -0.0f;
 
 // SIMD of the calling wave (HW_ID.SIMD_ID, bits [5:4]).
 __device__ __forceinline__ int wave_simd() { return (__builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11))) & 3; }

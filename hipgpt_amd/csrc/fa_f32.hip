@@ -157,10 +157,25 @@ struct F32Traits {
 // measured on MI355X with waves ranked by SIMD: D=32 2x2 (c1), D=64 4x2 (c3),
 // D=128 8x1 (c4) -- the larger head dims run 2 waves per SIMD, and more query
 // sub-blocks per workgroup share each K/V stage.
-template <int DP, int NQS, int NKS>
+template <int DP, int NQS, int NKS, bool CAUSAL_INST = true>
 hipError_t launch_dp(const AttnArgs& a, bool causal, bool probs, bool vec, hipStream_t s) {
-    return vec ? fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, true>(a, causal, probs, s)
-               : fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, false>(a, causal, probs, s);
+    return vec ? fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, true, CAUSAL_INST>(a, causal, probs, s)
+               : fa::launch_fa_flags<F32Traits<DP>, NQS, NKS, false, CAUSAL_INST>(a, causal, probs, s);
+}
+
+// D = 64 without a causal mask: where the 4 x 2 grid needs more than one
+// round of resident workgroups, 4 x 1 workgroups (the same 128 queries, no
+// key split, half the CU each, so twice as many resident).  Cache-rotated:
+// B8 H12 S1024 (768 workgroups on 512 4 x 2 slots) 206.5 -> 198.3 us, the
+// HipGPT drop-in there 324.9 -> 320.4 us.  Causal grids measured slower with
+// 4 x 1 at every size tried (c3 127 -> 140 us, B16 H12 S1024 229 -> 249,
+// c3 with probs 226 -> 245, S = 256 31.1 -> 33.0): their longest rows,
+// unsplit, set the end.
+bool dp64_narrow(const AttnArgs& a, bool causal) {
+    if (causal) return false;
+    const int64_t grid = (int64_t)((a.Sq + 127) / 128) * a.B * a.H;
+    const int slots = fa::fa_resident_slots<F32Traits<64>, 4, 2, false, true>();
+    return slots > 0 && grid > slots;
 }
 
 }  // namespace
@@ -236,7 +251,9 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
         return fa::launch_resident<F32Traits<64, true>, 8, 4>(a, causal, stream);
     switch (fa_f32_padded_dim(a.D)) {
         case 32: return launch_dp<32, 2, 2>(a, causal, probs, vec, stream);
-        case 64: return launch_dp<64, 4, 2>(a, causal, probs, vec, stream);
+        case 64:
+            return dp64_narrow(a, causal) ? launch_dp<64, 4, 1, false>(a, causal, probs, vec, stream)
+                                          : launch_dp<64, 4, 2>(a, causal, probs, vec, stream);
         case 128: return launch_dp<128, 8, 1>(a, causal, probs, vec, stream);
         default: return hipErrorInvalidValue;
     }

@@ -394,7 +394,7 @@ struct FaKernel {
                             for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
                         m_run = m_new;
                     }
-                    float lsum = 0.f;
+                    float lsum = kSumInit;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         sv[r] = fast_exp2(fmaf(sv[r], sc, -m_run));
@@ -408,7 +408,7 @@ struct FaKernel {
                 } else {
                     // the sum test of kLazySum; the max test only when it fails,
                     // with the scores recomputed from the staged K tile
-                    ls = 0.f;
+                    ls = kSumInit;
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
@@ -428,7 +428,7 @@ struct FaKernel {
                 else if (SPILL && qi < Sq)
                     store_probs_tile(prow, s, t * BK, hf, Sk, pvec);
                 const float m_new = vmax(m_run, tile_max(s) * sc);
-                float ls = 0.f;
+                float ls = kSumInit;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(s[r], sc, -m_new));
                 l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
@@ -464,7 +464,7 @@ struct FaKernel {
                     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
                 m_run = m_new;
             }
-            float ls = 0.f;
+            float ls = kSumInit;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
@@ -556,7 +556,7 @@ struct FaKernel {
                 const floatx16 sv = tile_scores(cur, t);
                 sres[I] = sv;
                 const float m_new = vmax(m_run, tile_max(sv) * sc);
-                float ls = 0.f;
+                float ls = kSumInit;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(sv[r], sc, -m_new));
                 l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);
@@ -844,28 +844,48 @@ struct probs_res_stages<TR, std::void_t<decltype(TR::PROBS_RES_STAGES)>> {
     static constexpr int value = TR::PROBS_RES_STAGES;
 };
 
-template <class TR, int NQS, int NKS, bool VEC>
+// Instances of one workgroup shape chosen by the runtime flags.  CAUSAL_INST
+// false: the caller launches it without a causal mask only, and no causal
+// instance is compiled.
+template <class TR, int NQS, int NKS, bool VEC, bool CAUSAL_INST = true>
 hipError_t launch_fa_flags(const AttnArgs& a, bool causal, bool probs, hipStream_t s) {
     constexpr int SRT = probs_res_stages<TR>::value;
     constexpr bool kSpill = VEC && sizeof(typename TR::elem) == 4 && TR::DP >= kScoreSpillMinDP;
+    if constexpr (!CAUSAL_INST) {
+        if (causal) return hipErrorInvalidValue;
+    }
+    // causal and non-causal instances of one choice of PROBS and SRT
+    auto by_mask = [&](auto probs_tag, auto srt_tag) -> hipError_t {
+        constexpr bool P = decltype(probs_tag)::value;
+        constexpr int R = decltype(srt_tag)::value;
+        if constexpr (CAUSAL_INST) {
+            if (causal) return launch_fa<TR, NQS, NKS, true, P, VEC, R>(a, s);
+        }
+        return launch_fa<TR, NQS, NKS, false, P, VEC, R>(a, s);
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
     if constexpr (SRT > 0) {
         // every wave's key tiles fit the resident stages (Sk <= SRT * NKS * 32)
         if (probs && ((a.Sk + BK - 1) / BK + NKS - 1) / NKS <= SRT)
-            return causal ? launch_fa<TR, NQS, NKS, true, true, VEC, SRT>(a, s)
-                          : launch_fa<TR, NQS, NKS, false, true, VEC, SRT>(a, s);
+            return by_mask(yes{}, std::integral_constant<int, SRT>{});
     }
     // longer rows: the scores are spilled to the probs buffer between the
     // sweeps (16-byte aligned probs rows)
     if constexpr (kSpill) {
         if (probs && (a.Sk & 3) == 0 && (reinterpret_cast<uintptr_t>(a.probs) & 15) == 0)
-            return causal ? launch_fa<TR, NQS, NKS, true, true, VEC, -1>(a, s)
-                          : launch_fa<TR, NQS, NKS, false, true, VEC, -1>(a, s);
+            return by_mask(yes{}, std::integral_constant<int, -1>{});
     }
-    if (causal)
-        return probs ? launch_fa<TR, NQS, NKS, true, true, VEC>(a, s)
-                     : launch_fa<TR, NQS, NKS, true, false, VEC>(a, s);
-    return probs ? launch_fa<TR, NQS, NKS, false, true, VEC>(a, s)
-                 : launch_fa<TR, NQS, NKS, false, false, VEC>(a, s);
+    return probs ? by_mask(yes{}, std::integral_constant<int, 0>{}) : by_mask(no{}, std::integral_constant<int, 0>{});
+}
+
+// Workgroups of one shape's plain instance (no probs) the device holds at
+// once, cached per device; 0 if the occupancy query fails.
+template <class TR, int NQS, int NKS, bool CAUSAL, bool VEC>
+int fa_resident_slots() {
+    static ResidentSlots cache;
+    return cache.get(reinterpret_cast<const void*>(fa_fwd_kernel<TR, NQS, NKS, CAUSAL, false, VEC, 0>), NQS * NKS * 64,
+                     0);
 }
 
 }  // namespace fa

@@ -206,7 +206,7 @@ struct FaResident {
                     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
                 m_run = m_new;
             }
-            float ls = 0.f;
+            float ls = kSumInit;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 s[r] = fast_exp2(fmaf(s[r], sc, -m_run));
@@ -218,7 +218,7 @@ struct FaResident {
         auto stats = [&](int t) {
             const floatx16 s = scores(t);
             const float m_new = vmax(m_run, tile_max(s) * sc);
-            float ls = 0.f;
+            float ls = kSumInit;
 #pragma unroll
             for (int r = 0; r < 16; ++r) ls += fast_exp2(fmaf(s[r], sc, -m_new));
             l_run = l_run * fast_exp2(m_run - m_new) + halves_sum(ls);

@@ -147,7 +147,7 @@ struct WideFwd {
                                 for (int r = 0; r < 16; ++r) o[0][db][r] *= alpha;
                             m_run = m_new;
                         }
-                        float ls = 0.f;
+                        float ls = fa::kSumInit;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             s[r] = fast_exp2(s[r] - m_run);
@@ -157,7 +157,7 @@ struct WideFwd {
                         T::template rchain<1>(o, vt, &s, c, hf, dh);
                     } else if constexpr (MODE == 1) {
                         const float m_new = fa::vmax(m_run, fa::tile_max(s));
-                        float ls = 0.f;
+                        float ls = fa::kSumInit;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) ls += fast_exp2(s[r] - m_new);
                         l_run = l_run * fast_exp2(m_run - m_new) + fa::halves_sum(ls);

@@ -71,7 +71,7 @@ struct RowTiles {
                                                      int lane) {
         floatx16 t;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) t[r] = 0.f;
+        for (int r = 0; r < 16; ++r) t[r] = fa::kSumInit;
 #pragma unroll
         for (int j = 0; j < DH; ++j) {
             floatx16 p;

@@ -134,6 +134,26 @@ def test_bf16_c3_fullsize_matches_f64(dev, causal):
     assert dmax(got, dev_t(want)) <= TOL_BF16
 
 
+@pytest.mark.parametrize("B,H,S,D,causal", [(16, 12, 1024, 64, True), (4, 16, 2048, 128, True),
+                                             (64, 8, 512, 32, True), (4, 16, 2048, 128, False),
+                                             (32, 8, 512, 32, False)])
+def test_bf16_grids_past_one_round_match_f64(dev, B, H, S, D, causal):
+    """bf16 grids larger than one round of resident workgroups, which take
+    workgroups of 4 query sub-blocks without a key split (causal: more
+    workgroups than the device holds of that shape; non-causal: more than it
+    holds of the split shape), every (b, h), against the float64 closed form
+    on the bf16-rounded inputs.  (c3 without a causal mask is one too.)"""
+    print(f"\n[bf16 past one round] B={B} H={H} S={S} D={D} causal={causal}", flush=True)
+    q, k, v = O.seeded_bshd(SEED + 17 * D + B, B, S, S, H, D)
+    tq, tk, tv = (dev_t(x).to(torch.bfloat16) for x in (q, k, v))
+    rq, rk, rv = (t.float().cpu().numpy() for t in (tq, tk, tv))
+    want, _ = O.attention(rq, rk, rv, causal=causal, f64=True, nthreads=NT)
+    got = A.attention(tq, tk, tv, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all().item()
+    assert dmax(got, dev_t(want)) <= TOL_BF16
+
+
 @pytest.mark.parametrize("splits", [None, 4])
 def test_decode_c5_fullsize(dev, splits):
     """c5 (B=64, H=12, one query against 2048 keys): all 768 rows against the
