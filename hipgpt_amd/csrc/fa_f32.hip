@@ -171,6 +171,24 @@ hipError_t launch_dp(const AttnArgs& a, bool causal, bool probs, bool vec, hipSt
 // 4 x 1 at every size tried (c3 127 -> 140 us, B16 H12 S1024 229 -> 249,
 // c3 with probs 226 -> 245, S = 256 31.1 -> 33.0): their longest rows,
 // unsplit, set the end.
+// D = 32 causal without probs on rows of at most 256 keys (at most four
+// query blocks of 64): where the grid exceeds one round of 2 x 1 workgroups
+// (64 queries, no key split, 2 waves), those instead of 2 x 2 -- the key
+// split's merge and per-workgroup stage then cost more than its shorter
+// rows save, the dispatch balancing the many rounds.  Cache-rotated (G
+// workgroups against 2048 2 x 1 slots): c1's shape at B = 128 (G 4096)
+// 59.6 -> 54.1 us, B = 256 115.7 -> 109.0; level or slower at B = 48 / 64
+// (28.0 / 28.0, 32.5 / 32.0), with probs (B = 128: 101.9 -> 137.7), without
+// a causal mask (85.5 / 85.6), and on longer rows (S = 512 B32: 48.9 ->
+// 51.5, S = 1024 B8 47.5 -> 64.5, B32 154.8 -> 153.0); c1 itself (G 1024)
+// 16.7 -> 20.6.
+bool dp32_unsplit(const AttnArgs& a, bool causal, bool probs, bool vec) {
+    if (!causal || probs || !vec || a.Sq > 256 || a.Sk > 256) return false;
+    const int64_t grid = (int64_t)((a.Sq + 63) / 64) * a.B * a.H;
+    const int slots = fa::fa_resident_slots<F32Traits<32>, 2, 1, true, true>();
+    return slots > 0 && grid > slots;
+}
+
 bool dp64_narrow(const AttnArgs& a, bool causal) {
     if (causal) return false;
     const int64_t grid = (int64_t)((a.Sq + 127) / 128) * a.B * a.H;
@@ -250,7 +268,9 @@ hipError_t launch_fa_f32(const AttnArgs& a, bool causal, bool vec, hipStream_t s
         (int64_t)a.B * a.H >= device_cus() && fa::resident_lds_bytes<F32Traits<64, true>, 8>(a) != 0)
         return fa::launch_resident<F32Traits<64, true>, 8, 4>(a, causal, stream);
     switch (fa_f32_padded_dim(a.D)) {
-        case 32: return launch_dp<32, 2, 2>(a, causal, probs, vec, stream);
+        case 32:
+            if (dp32_unsplit(a, causal, probs, vec)) return fa::launch_fa<F32Traits<32>, 2, 1, true, false, true>(a, stream);
+            return launch_dp<32, 2, 2>(a, causal, probs, vec, stream);
         case 64:
             return dp64_narrow(a, causal) ? launch_dp<64, 4, 1, false>(a, causal, probs, vec, stream)
                                           : launch_dp<64, 4, 2>(a, causal, probs, vec, stream);

@@ -203,3 +203,10 @@ def test_c1_head_shape_other_batches(dev, B, causal):
     out2 = nan_like((B * S, E), dev)
     A.qkv_planar(d_qkv, out2, None, B, S, E, H, causal=causal)
     assert dmax(out2, w_o) <= TOL_O
+    if causal:
+        # the forward that writes the row log-sum-exp (training without probs)
+        out3 = nan_like((B * S, E), dev)
+        lse = nan_like((B * H * S,), dev)
+        A.fwd_lse_qkv_planar(d_qkv, out3, lse, B, S, E, H, causal=True)
+        assert dmax(out3, w_o) <= TOL_O
+        assert torch.isfinite(lse).all().item()
