@@ -50,6 +50,10 @@ struct AttnArgs {
     // the first set the device holds at once -- delay their first loads by
     // their launch rank; 0 = no stagger.
     int stagger_slots;
+    // Late-block Q prefetch (set by the launcher for causal grids larger
+    // than the device holds at once): a workgroup of launch rank r touches
+    // the Q rows of rank r + pf_ranks; 0 = none.
+    int pf_ranks;
 };
 
 // 16-byte chunks of `rows` consecutive rows (row stride ts floats) through a

@@ -115,6 +115,17 @@ struct FaKernel {
     // guarded-load instances (padded head dims) spill registers with it
     // (25 at D = 128) and keep the max test.
     static constexpr bool SUM_CHECK = VEC;
+    // Causal grids larger than the device holds at once start their last
+    // launch ranks (the shortest query blocks) as slots free, well into the
+    // call, on Q rows nobody has read: each workgroup of rank r reads the Q
+    // rows of rank r + pf_ranks (same (b, h), same XCD) once during its
+    // second stage, one 4-byte load per 64 bytes of row, so those rows come
+    // from the caches when that workgroup starts.  Cache-rotated, two
+    // interleaved repetitions: c3-bf16 29.7 -> 28.5 us, bf16 B16 H12 S1024
+    // 49.7 -> 46.7, c3 127.6 -> 127.1, fp32 B16 H12 S1024 229.5 -> 227.7;
+    // fp32 D = 32 (B32 H8 S1024 155.8 -> 157.0) and D = 128 (c4 577 -> 579)
+    // measured level or slower and go without.
+    static constexpr bool PF_LATE = CAUSAL && !PROBS && (sizeof(E) == 2 || DP == 64);
     // Score-resident sweeps over at most two stages at D = 32 (the small
     // problems' 1 x 4 workgroups: HipGPT's generation call): K and V of both
     // stages are requested at once into the two stage buffers, so neither
@@ -280,6 +291,23 @@ struct FaKernel {
         const TileRange tr = tile_range<CAUSAL>(q0, qw0, NQS * QW, Sq, Sk, off);
         const int nstages = (tr.ntiles + NKS - 1) / NKS;
         const int wtiles = tr.wtiles;
+
+        const uint32_t* pf_ptr = nullptr;  // PF_LATE: this thread's 4 bytes of a later block's Q rows
+        if (PF_LATE && a.pf_ranks > 0 && rank + a.pf_ranks < a.n_qblk) {
+            const int pqb = a.n_qblk - 1 - (rank + a.pf_ranks);
+            constexpr int LPR = (DP * (int)sizeof(E) + 63) / 64;  // 64-byte pieces per row
+            const int row = pqb * NQS * QW + tid / LPR, piece = tid % LPR;
+            if (tid < NQS * QW * LPR && row < Sq)
+                pf_ptr = reinterpret_cast<const uint32_t*>(Qp + (int64_t)row * a.q_ts + piece * (64 / (int)sizeof(E)));
+        }
+        uint32_t pfv = 0;
+        // the load's result is kept (an empty asm reads it) one stage later
+        auto pf_issue = [&](int i) {
+            if (PF_LATE && i == 1 && pf_ptr) pfv = *pf_ptr;
+        };
+        auto pf_keep = [&](int i) {
+            if (PF_LATE && i == 1) asm volatile("" ::"v"(pfv));
+        };
 
         typename TR::QReg qreg;
         TR::template load_q<VEC>(qreg, Qp + (int64_t)qi * a.q_ts, hf, qi < Sq, a.D, a.qscale);
@@ -509,8 +537,10 @@ struct FaKernel {
                 }
                 for (int i = 1; i < nstages; ++i) {
                     if (i + 1 < nstages) st.template load<true, true>(i + 1, tid);
+                    pf_issue(i);
                     compute(mode_tag, i, mlog, prow, pvec);
                     if (i + 1 < nstages) st.template store<true, true>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                    pf_keep(i);
                     __syncthreads();
                 }
                 return;
@@ -536,8 +566,10 @@ struct FaKernel {
             } else {
                 for (int i = 0; i < nstages; ++i) {
                     if (i + 1 < nstages) st.template load<WV, WK>(i + 1, tid);
+                    if (MODE == 0) pf_issue(i);
                     compute(mode_tag, i, mlog, prow, pvec);
                     if (i + 1 < nstages) st.template store<WV, WK>(lds + ((i + 1) & 1) * STAGE_ELEMS, tid);
+                    if (MODE == 0) pf_keep(i);
                     __syncthreads();
                 }
             }
@@ -814,12 +846,19 @@ hipError_t launch_fa(const AttnArgs& a, hipStream_t stream) {
     const int64_t grid = (int64_t)args.n_qblk * a.B * a.H;
     if (grid <= 0 || grid > 0x7fffffff) return hipErrorInvalidConfiguration;
     auto kern = fa_fwd_kernel<TR, NQS, NKS, CAUSAL, PROBS, VEC, SRT>;
+    static ResidentSlots cache;  // workgroups of this instance the device holds at once
     args.stagger_slots = 0;
     if ((CAUSAL || PROBS) && args.n_qblk > 1 && args.n_qblk <= kStaggerMaxBlocks) {
-        static ResidentSlots cache;
         const int slots = cache.get(reinterpret_cast<const void*>(kern), NQS * NKS * 64, 0);
         // only grids the device holds at once, filling at least half of it
         if (slots > 0 && 2 * grid >= slots && grid <= slots) args.stagger_slots = slots;
+    }
+    args.pf_ranks = 0;
+    if (FaKernel<TR, NQS, NKS, CAUSAL, PROBS, VEC, SRT>::PF_LATE) {
+        // the first round holds slots / (B*H) whole launch ranks
+        const int slots = cache.get(reinterpret_cast<const void*>(kern), NQS * NKS * 64, 0);
+        const int64_t bh = (int64_t)a.B * a.H;
+        if (slots > 0 && grid > slots && slots >= bh) args.pf_ranks = (int)(slots / bh);
     }
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NQS * NKS * 64), 0, stream, args);
     return hipGetLastError();
