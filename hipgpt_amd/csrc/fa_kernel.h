@@ -297,8 +297,9 @@ struct FaKernel {
             const int pqb = a.n_qblk - 1 - (rank + a.pf_ranks);
             constexpr int LPR = (DP * (int)sizeof(E) + 63) / 64;  // 64-byte pieces per row
             const int row = pqb * NQS * QW + tid / LPR, piece = tid % LPR;
-            if (tid < NQS * QW * LPR && row < Sq)
-                pf_ptr = reinterpret_cast<const uint32_t*>(Qp + (int64_t)row * a.q_ts + piece * (64 / (int)sizeof(E)));
+            const int col = piece * (64 / (int)sizeof(E));  // inside the row's D elements only
+            if (tid < NQS * QW * LPR && row < Sq && col < a.D)
+                pf_ptr = reinterpret_cast<const uint32_t*>(Qp + (int64_t)row * a.q_ts + col);
         }
         uint32_t pfv = 0;
         // the load's result is kept (an empty asm reads it) one stage later

@@ -154,6 +154,21 @@ def test_bf16_grids_past_one_round_match_f64(dev, B, H, S, D, causal):
     assert dmax(got, dev_t(want)) <= TOL_BF16
 
 
+@pytest.mark.parametrize("D", [48, 64])
+def test_causal_grid_past_one_round_matches_oracle(dev, D):
+    """Causal fp32 grids larger than the device holds at once, where the
+    early launch ranks read the late ones' Q rows ahead (a padded head dim,
+    D = 48, reads only its D columns); every (b, h) against the oracle."""
+    B, H, S = 16, 12, 1024
+    print(f"\n[causal past one round] B={B} H={H} S={S} D={D}", flush=True)
+    q, k, v = O.seeded_bshd(SEED + 31 * D, B, S, S, H, D)
+    want, _ = O.attention(q, k, v, causal=True, nthreads=NT)
+    got = A.attention(dev_t(q), dev_t(k), dev_t(v), causal=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all().item()
+    assert dmax(got, dev_t(want)) <= TOL_O
+
+
 @pytest.mark.parametrize("splits", [None, 4])
 def test_decode_c5_fullsize(dev, splits):
     """c5 (B=64, H=12, one query against 2048 keys): all 768 rows against the
