@@ -121,8 +121,8 @@ struct FaKernel {
     // rows of rank r + pf_ranks (same (b, h), same XCD) once during its
     // second stage, one 4-byte load per 64 bytes of row, so those rows come
     // from the caches when that workgroup starts.  Cache-rotated, two
-    // interleaved repetitions: c3-bf16 29.7 -> 28.5 us, bf16 B16 H12 S1024
-    // 49.7 -> 46.7, c3 127.6 -> 127.1, fp32 B16 H12 S1024 229.5 -> 227.7;
+    // interleaved repetitions: c3-bf16 29.7 -> 29.1 us, bf16 B16 H12 S1024
+    // 50.0 -> 47.2, c3 127.0 -> 126.5, fp32 B16 H12 S1024 228.6 -> 226.4;
     // fp32 D = 32 (B32 H8 S1024 155.8 -> 157.0) and D = 128 (c4 577 -> 579)
     // measured level or slower and go without.
     static constexpr bool PF_LATE = CAUSAL && !PROBS && (sizeof(E) == 2 || DP == 64);
