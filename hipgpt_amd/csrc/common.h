@@ -54,6 +54,10 @@ struct AttnArgs {
     // than the device holds at once): a workgroup of launch rank r touches
     // the Q rows of rank r + pf_ranks; 0 = none.
     int pf_ranks;
+    // Causal launch order (set by the launcher): launch rank short_rank - 1
+    // runs the shortest query block, the others the rest longest first; 0 =
+    // plain longest-first (the zero-initialised default).
+    int short_rank;
 };
 
 // 16-byte chunks of `rows` consecutive rows (row stride ts floats) through a
